@@ -1,0 +1,150 @@
+#!/usr/bin/env python3
+"""Prefill tok/s and ms/verdict for a 1024-token prompt on a Shieldstral-3B-shaped Q4_0 model.
+
+One step = one verdict: reset the KV cache, prefill 1024 token ids through all 26 layers
+on the GPU, evaluate the yes/no rows of the tied LM head at the last position, and
+compute the Score on the host (ShieldstralModerator.ModerateAsync without tokenization).
+Weights are a random-init model of the real architecture built in HBM (synthetic data);
+token ids are uniform over the vocabulary. Single GPU only.
+
+Prints one JSON line; see --help for options.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "llm-shield_amd"))
+
+METRIC = "prefill tok/s + ms/verdict (1k-token prompt), Shieldstral-3B Q4_0, 1 MI355X"
+T_PROMPT = 1024
+PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
+PEAK_HBM_GBS = 8000.0
+
+
+def gemm_flops_per_layer(cfg, T):
+    h, q, kv, f = cfg.hidden_size, cfg.q_dim, cfg.kv_dim, cfg.feed_forward_size
+    return 2.0 * T * h * (q + 2 * kv) + 2.0 * T * q * h + 2.0 * T * h * 2 * f + 2.0 * T * f * h
+
+
+def cpu_baseline(model, cfg, T, seed):
+    """The oracle (C restatement of the reference CPU path) on one decoder layer at T tokens,
+    scaled to the 26-layer prompt: a bounded sample of the same workload."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
+    import oracle as O
+
+    one = O.make_config(n_layer=1, hidden=cfg.hidden_size, n_head=cfg.head_count, n_kv_head=cfg.kv_head_count,
+                        head_dim=cfg.head_dim, ffn=cfg.feed_forward_size, vocab=cfg.vocab_size,
+                        rope_theta=cfg.rope_freq_base)
+    names = [n for n in cfg.tensor_shapes(2, 2) if n.startswith("blk.0.")]
+    tensors = {n: model.download(n) for n in names}
+    types = {n: (0 if n.endswith("norm.weight") else 2) for n in names}
+    tensors["token_embd.weight"] = np.zeros(1, np.uint8)
+    tensors["output_norm.weight"] = np.ones(cfg.hidden_size, np.float32)
+    types["token_embd.weight"], types["output_norm.weight"] = 2, 0
+    om = O.OracleModel(one, tensors, types, cap=T)
+    x = np.random.default_rng(seed).standard_normal((T, cfg.hidden_size)).astype(np.float32) * 0.02
+    threads = os.cpu_count() or 1
+    om.layer_forward(0, x[:64], threads=threads)  # warm-up
+    t0 = time.perf_counter()
+    om.layer_forward(0, x, threads=threads)
+    layer_s = time.perf_counter() - t0
+    total_s = layer_s * cfg.layer_count
+    return {"value": round(T / total_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"oracle (C restatement of the reference CPU path, OpenMP over rows) on 1 of "
+                      f"{cfg.layer_count} decoder layers at T={T}: {layer_s:.2f} s, scaled x{cfg.layer_count}",
+            "ms_per_verdict": round(total_s * 1e3, 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--tokens", type=int, default=T_PROMPT)
+    ap.add_argument("--seed", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the verdict path does not shard "
+              f"across GPUs in this build.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import shieldstral as S
+
+    cfg = S.SHIELDSTRAL_3B
+    T = args.tokens
+    model = S.MinistralModel.synthetic(cfg, S.Q4_0, seed=args.seed, initial_cache_capacity=T)
+    rng = np.random.default_rng(args.seed)
+    tokens = rng.integers(0, cfg.vocab_size, T).astype(np.int32)
+    yes, no = (int(v) for v in rng.choice(cfg.vocab_size, 2, replace=False))
+    ids = [yes, no]
+
+    def step():
+        model.reset_kv_cache()
+        logits = model.forward_selected(tokens, ids)
+        return S.score(logits, 1, T, 0)
+
+    for _ in range(args.warmup):
+        step()
+    model.profile_reset()
+    model.profile(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        result = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    model.profile(False)
+    ms = elapsed / args.steps * 1e3
+
+    n, gemm_ms, gemm_ops = model.profile_read("gemm")
+    achieved = gemm_ops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
+    breakdown = {}
+    for cls in ("gemm", "attention", "rmsnorm_quant", "swiglu_quant", "quant_act", "rope_store", "embed", "gemv"):
+        c, cms, _ = model.profile_read(cls)
+        if c:
+            breakdown[cls] = {"launches_per_step": c // args.steps, "ms_per_step": round(cms / args.steps, 4)}
+
+    line = {
+        "metric": METRIC,
+        "value": round(T / (ms * 1e-3), 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "ms_per_verdict": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"Shieldstral-3B-shaped random-init Q4_0 model, 1 prompt of {T} token ids, "
+                               f"prefill + yes/no head rows + Score",
+                   "layers": cfg.layer_count, "hidden": cfg.hidden_size, "ffn": cfg.feed_forward_size,
+                   "heads": cfg.head_count, "kv_heads": cfg.kv_head_count, "vocab": cfg.vocab_size,
+                   "tokens": T, "weights": "Q4_0", "seed": args.seed},
+        "roofline": {"bound": "mfma", "kernel": "k_gemm (int8 MFMA, all projections)",
+                     "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "launches": n, "ms_per_launch": round(gemm_ms / max(n, 1), 5),
+                     "ops_per_launch": round(gemm_ops / max(n, 1))},
+        "breakdown": breakdown,
+        "score": result.score,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(model, cfg, T, args.seed)
+    model.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

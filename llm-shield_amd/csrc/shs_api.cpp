@@ -1,0 +1,1338 @@
+// libshieldstral_hip host runtime: the C ABI of include/shieldstral_hip.h.
+//
+// Owns device memory, one HIP stream per handle, the KV cache and the forward-pass
+// orchestration of MinistralModel.ForwardAsync (MinistralModel.cs:183-271), issuing
+// the gfx950 kernels of shs_kernels.hip. No CPU fallback exists: without a gfx950
+// device every entry point that needs one fails with SHS_E_DEVICE.
+#include "shieldstral_hip.h"
+#include "shs_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+using namespace shs;
+
+// ----------------------------------------------------------------- errors
+
+static thread_local std::string g_error;
+
+static shs_status fail(shs_status code, const char* fmt, ...)
+{
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+static shs_status hip_fail(hipError_t e, const char* what)
+{
+    return fail(SHS_E_DEVICE, "%s failed: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                            \
+    do {                                                         \
+        hipError_t e_ = (expr);                                  \
+        if (e_ != hipSuccess) return hip_fail(e_, #expr);        \
+    } while (0)
+
+extern "C" const char* shs_last_error(void) { return g_error.c_str(); }
+
+// ------------------------------------------------------------- device bufs
+
+namespace {
+
+struct Buf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    ~Buf() { release(); }
+    void release()
+    {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    hipError_t ensure(size_t n)
+    {
+        if (n <= bytes) return hipSuccess;
+        release();
+        hipError_t e = hipMalloc(&p, n);
+        if (e == hipSuccess) bytes = n;
+        else p = nullptr;
+        return e;
+    }
+    template <class T> T* as() const { return static_cast<T*>(p); }
+};
+
+struct ActBuf {
+    Buf q, d, ds;
+    hipError_t ensure(int T, int K, ActQ8* view)
+    {
+        int Tpad = (T + 31) / 32 * 32;
+        int B = K / 32;
+        hipError_t e;
+        if ((e = q.ensure((size_t)Tpad * K)) != hipSuccess) return e;
+        if ((e = d.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
+        if ((e = ds.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
+        view->T = T;
+        view->Tpad = Tpad;
+        view->K = K;
+        view->B = B;
+        view->q = q.as<int8_t>();
+        view->d = d.as<float>();
+        view->ds = ds.as<float>();
+        return hipSuccess;
+    }
+};
+
+void free_matrix(DevMatrix& m)
+{
+    if (m.qs) (void)hipFree(m.qs);
+    if (m.qh) (void)hipFree(m.qh);
+    if (m.d) (void)hipFree(m.d);
+    if (m.m) (void)hipFree(m.m);
+    m = DevMatrix();
+}
+
+hipError_t alloc_matrix(DevMatrix& m, int type, int rows, int cols)
+{
+    m.type = type;
+    m.rows = rows;
+    m.cols = cols;
+    m.blocks = cols / 32;
+    m.tiles = (rows + 31) / 32;
+    size_t recs = (size_t)m.tiles * m.blocks;
+    hipError_t e;
+    if ((e = hipMalloc((void**)&m.qs, recs * 32 * qs_bytes(type))) != hipSuccess) return e;
+    if ((e = hipMemset(m.qs, 0, recs * 32 * qs_bytes(type))) != hipSuccess) return e;
+    if ((e = hipMalloc((void**)&m.d, recs * 32 * sizeof(float))) != hipSuccess) return e;
+    if ((e = hipMemset(m.d, 0, recs * 32 * sizeof(float))) != hipSuccess) return e;
+    if (type_has_qh(type)) {
+        if ((e = hipMalloc((void**)&m.qh, recs * 32 * sizeof(uint32_t))) != hipSuccess) return e;
+        if ((e = hipMemset(m.qh, 0, recs * 32 * sizeof(uint32_t))) != hipSuccess) return e;
+    }
+    if (type_has_offset(type)) {
+        if ((e = hipMalloc((void**)&m.m, recs * 32 * sizeof(float))) != hipSuccess) return e;
+        if ((e = hipMemset(m.m, 0, recs * 32 * sizeof(float))) != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+int64_t row_bytes(int type, int64_t cols)
+{
+    int ts = type == SHS_Q4_0 ? 18 : type == SHS_Q4_1 ? 20 : type == SHS_Q5_0 ? 22 : type == SHS_Q5_1 ? 24
+           : type == SHS_Q8_0 ? 34 : -1;
+    return ts < 0 ? -1 : cols / 32 * ts;
+}
+
+const char* type_name(int t)
+{
+    switch (t) {
+    case 0: return "F32";
+    case 1: return "F16";
+    case 2: return "Q4_0";
+    case 3: return "Q4_1";
+    case 6: return "Q5_0";
+    case 7: return "Q5_1";
+    case 8: return "Q8_0";
+    default: return "unsupported";
+    }
+}
+
+// Where a tensor's native bytes come from: the caller's host buffer, or the synthetic
+// generator (N(mean, std) quantized on the device) when host is null.
+struct Source {
+    const void* host = nullptr;
+    uint64_t seed = 0, id = 0;
+    float mean = 0.0f, std = 0.0f;
+};
+
+// Uploads (or generates) a native-layout tensor into rows [row0, row0+nrows) of a
+// repacked matrix through a device staging buffer.
+hipError_t upload_rows(DevMatrix& m, const Source& src, int row0, int nrows, Buf& staging, hipStream_t s)
+{
+    size_t bytes = (size_t)nrows * (size_t)row_bytes(m.type, m.cols);
+    hipError_t e;
+    if ((e = staging.ensure(bytes)) != hipSuccess) return e;
+    if (src.host)
+        e = hipMemcpyAsync(staging.p, src.host, bytes, hipMemcpyHostToDevice, s);
+    else
+        e = launch_synth_native(m.type, src.seed, src.id, nrows, m.cols, src.mean, src.std, staging.as<uint8_t>(), s);
+    if (e != hipSuccess) return e;
+    if ((e = launch_repack(m, staging.as<uint8_t>(), row0, nrows, s)) != hipSuccess) return e;
+    return hipStreamSynchronize(s);
+}
+
+Source host_src(const void* p)
+{
+    Source s;
+    s.host = p;
+    return s;
+}
+
+bool device_is_gfx950(int device, std::string* arch)
+{
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
+    *arch = prop.gcnArchName;
+    return arch->rfind("gfx950", 0) == 0;
+}
+
+shs_status select_device(int device)
+{
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0)
+        return fail(SHS_E_DEVICE, "no HIP device is visible (%s); libshieldstral_hip runs only on a gfx950 (MI355X) GPU",
+                    hipGetErrorString(e));
+    if (device < 0 || device >= count)
+        return fail(SHS_E_INVALID_ARGUMENT, "device %d does not exist (%d visible)", device, count);
+    std::string arch;
+    if (!device_is_gfx950(device, &arch))
+        return fail(SHS_E_DEVICE, "device %d is %s; these kernels are built for gfx950 (MI355X) only", device, arch.c_str());
+    HIP_TRY(hipSetDevice(device));
+    return SHS_OK;
+}
+
+// Kernel-class timing with events on the launching stream.
+struct Profiler {
+    bool on = false;
+    struct Rec {
+        hipEvent_t a, b;
+        std::string cls;
+        double ops;
+    };
+    std::vector<Rec> pending;
+    std::map<std::string, std::pair<int64_t, std::pair<double, double>>> totals;
+    std::vector<hipEvent_t> pool;
+    hipEvent_t get()
+    {
+        if (!pool.empty()) {
+            hipEvent_t e = pool.back();
+            pool.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        return e;
+    }
+    void begin(const char* cls, double ops, hipStream_t s, Rec* r)
+    {
+        r->a = get();
+        r->b = get();
+        r->cls = cls;
+        r->ops = ops;
+        if (r->a) (void)hipEventRecord(r->a, s);
+    }
+    void end(Rec& r, hipStream_t s)
+    {
+        if (r.b) (void)hipEventRecord(r.b, s);
+        pending.push_back(r);
+    }
+    void collect()
+    {
+        for (auto& r : pending) {
+            float ms = 0.0f;
+            if (r.a && r.b && hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
+                auto& t = totals[r.cls];
+                t.first += 1;
+                t.second.first += ms;
+                t.second.second += r.ops;
+            }
+            if (r.a) pool.push_back(r.a);
+            if (r.b) pool.push_back(r.b);
+        }
+        pending.clear();
+    }
+    ~Profiler()
+    {
+        for (auto& r : pending) {
+            if (r.a) (void)hipEventDestroy(r.a);
+            if (r.b) (void)hipEventDestroy(r.b);
+        }
+        for (auto e : pool) (void)hipEventDestroy(e);
+    }
+};
+
+// RAII scope that times one launch when profiling is on.
+struct Timed {
+    Profiler& p;
+    hipStream_t s;
+    Profiler::Rec rec{};
+    bool active;
+    Timed(Profiler& pr, const char* cls, double ops, hipStream_t st) : p(pr), s(st), active(pr.on)
+    {
+        if (active) p.begin(cls, ops, s, &rec);
+    }
+    ~Timed()
+    {
+        if (active) p.end(rec, s);
+    }
+};
+
+// A projection applied as one or more GEMMs writing adjacent column ranges of one
+// output (q|k|v and gate|up are fused into one matrix when their types agree).
+struct Proj {
+    std::vector<DevMatrix> parts;
+    std::vector<int> col0;
+    int out_cols = 0;
+};
+
+// Where a named tensor lives on the device (for shs_tensor_download).
+struct TensorLoc {
+    const DevMatrix* mat = nullptr;  // matrices: rows [row0, row0 + rows) of mat
+    int row0 = 0, rows = 0;
+    const float* vec = nullptr;      // norm gains: n floats
+    int n = 0;
+};
+
+struct Layer {
+    float* attn_norm = nullptr;
+    float* ffn_norm = nullptr;
+    Proj qkv, o, gu, down;
+};
+
+}  // namespace
+
+struct shs_matrix {
+    DevMatrix w;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    ActBuf act;
+    Buf x, y, ids, sums;
+};
+
+struct shs_model {
+    shs_config cfg{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    DevMatrix embd;
+    DevMatrix head;  // output.weight when present; otherwise the tied embedding
+    bool tied = true;
+    float* out_norm = nullptr;
+    std::vector<Layer> layers;
+    // KV cache: per layer [kv_head][cap][head_dim] fp32, keys then values.
+    float* kc = nullptr;
+    float* vc = nullptr;
+    int cap = 0, len = 0;
+    // RoPE tables (host-computed cos/sin of position·freq, Rope.cs:117-122).
+    std::vector<float> freqs;
+    float mscale = 1.0f;
+    int rope_cap = 0;
+    Buf cos_tab, sin_tab, qscale_tab;
+    // Work buffers, grown on demand.
+    Buf h, qkv, ctx, gu, tmp, normed, ffn_act, tokens, pos, items, ids, logits, last_rows, lastidx, bkc, bvc;
+    ActBuf act;
+    shs_capture_fn cap_fn = nullptr;
+    void* cap_user = nullptr;
+    Profiler prof;
+    std::map<std::string, TensorLoc> where;
+};
+
+// ------------------------------------------------------------------ RoPE
+
+static void rope_freqs(const shs_config& c, std::vector<float>& f, float& mscale)
+{
+    // Rope ctor (Rope.cs:33-66) and ComputeMagnitudeScale (Rope.cs:78-88).
+    int dim = c.rope_dim, half = dim / 2;
+    f.assign(half, 0.0f);
+    float freq_scale = 1.0f / c.rope_scale;
+    if (!c.yarn_active) {
+        for (int i = 0; i < half; i++) f[i] = freq_scale / powf(c.rope_theta, 2.0f * (float)i / (float)dim);
+        mscale = c.rope_attn_factor;
+        return;
+    }
+    float low, high;
+    if (c.yarn_beta_fast == 0.0f && c.yarn_beta_slow == 0.0f) {
+        low = 3.40282347e38f;
+        high = (float)dim / 2.0f - 1.0f;
+    } else {
+        const float PI = 3.14159265358979323846f;
+        float cf = (float)dim * logf((float)c.rope_orig_ctx / (c.yarn_beta_fast * 2.0f * PI)) / (2.0f * logf(c.rope_theta));
+        float cs = (float)dim * logf((float)c.rope_orig_ctx / (c.yarn_beta_slow * 2.0f * PI)) / (2.0f * logf(c.rope_theta));
+        low = fmaxf(0.0f, floorf(cf));
+        high = fminf((float)dim / 2.0f - 1.0f, ceilf(cs));
+    }
+    for (int i = 0; i < half; i++) {
+        float extrapolated = 1.0f / powf(c.rope_theta, 2.0f * (float)i / (float)dim);
+        float interpolated = freq_scale * extrapolated;
+        float y = ((float)i - low) / fmaxf(0.001f, high - low);
+        float cl = y < 0.0f ? 0.0f : (y > 1.0f ? 1.0f : y);
+        float mix = (1.0f - cl) * c.yarn_ext_factor;
+        float a = interpolated * (1.0f - mix);
+        float b = extrapolated * mix;
+        f[i] = a + b;
+    }
+    auto ms = [](float scale, float m) { return scale <= 1.0f ? 1.0f : 0.1f * m * logf(scale) + 1.0f; };
+    float factor = c.rope_scale;
+    float m0 = c.yarn_mscale != 0.0f ? c.yarn_mscale : 1.0f;
+    float ratio = c.yarn_mscale_all_dim != 0.0f ? ms(factor, m0) / ms(factor, c.yarn_mscale_all_dim) : ms(factor, 1.0f);
+    mscale = ratio * c.rope_attn_factor;
+}
+
+static shs_status ensure_rope(shs_model* m, int need)
+{
+    if (need <= m->rope_cap) return SHS_OK;
+    int cap = std::max(512, m->rope_cap);
+    while (cap < need) cap *= 2;
+    int half = m->cfg.rope_dim / 2;
+    std::vector<float> c((size_t)cap * half), s((size_t)cap * half), qs(cap);
+    for (int p = 0; p < cap; p++) {
+        for (int i = 0; i < half; i++) {
+            float theta = (float)p * m->freqs[i];
+            c[(size_t)p * half + i] = cosf(theta) * m->mscale;
+            s[(size_t)p * half + i] = sinf(theta) * m->mscale;
+        }
+        // ApplyPositionScale (MinistralModel.cs:476-482).
+        float scale = 1.0f;
+        if (m->cfg.rope_orig_ctx > 0 && m->cfg.attn_temperature != 0.0f) {
+            float interval = floorf((float)p / (float)m->cfg.rope_orig_ctx);
+            if (interval != 0.0f) scale = 1.0f + m->cfg.attn_temperature * logf(1.0f + interval);
+        }
+        qs[p] = scale;
+    }
+    HIP_TRY(m->cos_tab.ensure(c.size() * sizeof(float)));
+    HIP_TRY(m->sin_tab.ensure(s.size() * sizeof(float)));
+    HIP_TRY(m->qscale_tab.ensure(qs.size() * sizeof(float)));
+    HIP_TRY(hipMemcpy(m->cos_tab.p, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(m->sin_tab.p, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(m->qscale_tab.p, qs.data(), qs.size() * sizeof(float), hipMemcpyHostToDevice));
+    m->rope_cap = cap;
+    return SHS_OK;
+}
+
+// ---------------------------------------------------------------- KV cache
+
+static size_t kv_layer_floats(const shs_model* m, int cap)
+{
+    return (size_t)m->cfg.n_kv_head * cap * m->cfg.head_dim;
+}
+
+// KvCache.EnsureCapacity (KvCache.cs:48-70): doubles, keeping the first len positions.
+static shs_status ensure_kv(shs_model* m, int need)
+{
+    if (need <= m->cap) return SHS_OK;
+    int cap = std::max(1, m->cap);
+    while (cap < need) cap *= 2;
+    size_t per = kv_layer_floats(m, cap) * m->cfg.n_layer;
+    float *kc = nullptr, *vc = nullptr;
+    HIP_TRY(hipMalloc(&kc, per * sizeof(float)));
+    hipError_t e = hipMalloc(&vc, per * sizeof(float));
+    if (e != hipSuccess) {
+        (void)hipFree(kc);
+        return hip_fail(e, "hipMalloc(kv)");
+    }
+    if (m->len > 0 && m->kc) {
+        size_t hd = m->cfg.head_dim;
+        size_t rows = (size_t)m->cfg.n_layer * m->cfg.n_kv_head;
+        HIP_TRY(hipMemcpy2DAsync(kc, cap * hd * 4, m->kc, m->cap * hd * 4, m->len * hd * 4, rows, hipMemcpyDeviceToDevice, m->stream));
+        HIP_TRY(hipMemcpy2DAsync(vc, cap * hd * 4, m->vc, m->cap * hd * 4, m->len * hd * 4, rows, hipMemcpyDeviceToDevice, m->stream));
+        HIP_TRY(hipStreamSynchronize(m->stream));
+    }
+    if (m->kc) (void)hipFree(m->kc);
+    if (m->vc) (void)hipFree(m->vc);
+    m->kc = kc;
+    m->vc = vc;
+    m->cap = cap;
+    return SHS_OK;
+}
+
+// ------------------------------------------------------------------ open
+
+namespace {
+
+// One tensor to load: its GGUF name, type, shape [ne0 = in, ne1 = out] and byte source.
+struct Spec {
+    std::string name;
+    int type = 0;
+    int64_t ne0 = 0, ne1 = 0;
+    Source src;
+};
+
+struct SpecMap {
+    std::map<std::string, Spec> byname;
+    const Spec* get(const std::string& n) const
+    {
+        auto it = byname.find(n);
+        return it == byname.end() ? nullptr : &it->second;
+    }
+};
+
+shs_status need_tensor(const SpecMap& tm, const std::string& name, const Spec** out)
+{
+    *out = tm.get(name);
+    if (!*out) return fail(SHS_E_KEY_NOT_FOUND, "tensor '%s' is missing; this does not look like a Shieldstral GGUF", name.c_str());
+    return SHS_OK;
+}
+
+shs_status check_matrix(const Spec* t, int64_t in, int64_t out)
+{
+    if (!type_supported(t->type))
+        return fail(SHS_E_NOT_SUPPORTED,
+                    "tensor '%s' is %s; the integer GEMM takes Q4_0, Q4_1, Q5_0, Q5_1 and Q8_0 weights only",
+                    t->name.c_str(), type_name(t->type));
+    if (t->ne0 != in || t->ne1 != out)
+        return fail(SHS_E_INVALID_DATA, "tensor '%s' is [%lld x %lld]; the model's hyperparameters need [%lld x %lld]",
+                    t->name.c_str(), (long long)t->ne0, (long long)t->ne1, (long long)in, (long long)out);
+    return SHS_OK;
+}
+
+shs_status load_proj(shs_model* m, Proj& p, const std::vector<const Spec*>& ts, Buf& staging)
+{
+    bool same = true;
+    for (auto* t : ts) same = same && t->type == ts[0]->type;
+    int total = 0;
+    bool aligned = true;
+    for (auto* t : ts) {
+        aligned = aligned && total % 32 == 0;
+        total += (int)t->ne1;
+    }
+    p.out_cols = total;
+    p.parts.reserve(ts.size());
+    if (same && aligned) {
+        DevMatrix w;
+        HIP_TRY(alloc_matrix(w, ts[0]->type, total, (int)ts[0]->ne0));
+        p.parts.push_back(w);
+        p.col0.push_back(0);
+        int row0 = 0;
+        for (auto* t : ts) {
+            HIP_TRY(upload_rows(p.parts[0], t->src, row0, (int)t->ne1, staging, m->stream));
+            row0 += (int)t->ne1;
+        }
+        row0 = 0;
+        for (auto* t : ts) {
+            m->where[t->name] = TensorLoc{&p.parts[0], row0, (int)t->ne1, nullptr, 0};
+            row0 += (int)t->ne1;
+        }
+    } else {
+        int c0 = 0;
+        for (auto* t : ts) {
+            DevMatrix w;
+            HIP_TRY(alloc_matrix(w, t->type, (int)t->ne1, (int)t->ne0));
+            p.parts.push_back(w);
+            HIP_TRY(upload_rows(p.parts.back(), t->src, 0, (int)t->ne1, staging, m->stream));
+            p.col0.push_back(c0);
+            c0 += (int)t->ne1;
+        }
+        for (size_t i = 0; i < ts.size(); i++)
+            m->where[ts[i]->name] = TensorLoc{&p.parts[i], 0, (int)ts[i]->ne1, nullptr, 0};
+    }
+    return SHS_OK;
+}
+
+shs_status upload_vector(shs_model* m, const Spec* t, int64_t n, float** out)
+{
+    if (t->ne0 != n || t->ne1 != 1)
+        return fail(SHS_E_INVALID_DATA, "tensor '%s' has %lld elements; expected %lld", t->name.c_str(), (long long)(t->ne0 * t->ne1),
+                    (long long)n);
+    HIP_TRY(hipMalloc(out, n * sizeof(float)));
+    if (!t->src.host) {
+        HIP_TRY(launch_synth_f32(t->src.seed, t->src.id, n, t->src.mean, t->src.std, *out, m->stream));
+        HIP_TRY(hipStreamSynchronize(m->stream));
+    } else {
+        std::vector<float> v(n);
+        if (t->type == SHS_F32) {
+            memcpy(v.data(), t->src.host, n * sizeof(float));
+        } else if (t->type == SHS_F16) {
+            const uint16_t* h = static_cast<const uint16_t*>(t->src.host);
+            for (int64_t i = 0; i < n; i++) {
+                _Float16 x;
+                memcpy(&x, &h[i], 2);
+                v[i] = (float)x;
+            }
+        } else {
+            return fail(SHS_E_NOT_SUPPORTED, "norm tensor '%s' is %s; F32 or F16 expected", t->name.c_str(), type_name(t->type));
+        }
+        HIP_TRY(hipMemcpy(*out, v.data(), n * sizeof(float), hipMemcpyHostToDevice));
+    }
+    m->where[t->name] = TensorLoc{nullptr, 0, 0, *out, (int)n};
+    return SHS_OK;
+}
+
+void destroy_model(shs_model* m)
+{
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    free_matrix(m->embd);
+    if (!m->tied) free_matrix(m->head);
+    if (m->out_norm) (void)hipFree(m->out_norm);
+    for (auto& L : m->layers) {
+        if (L.attn_norm) (void)hipFree(L.attn_norm);
+        if (L.ffn_norm) (void)hipFree(L.ffn_norm);
+        for (Proj* p : {&L.qkv, &L.o, &L.gu, &L.down})
+            for (auto& w : p->parts) free_matrix(w);
+    }
+    if (m->kc) (void)hipFree(m->kc);
+    if (m->vc) (void)hipFree(m->vc);
+    hipStream_t s = m->stream;
+    delete m;
+    if (s) (void)hipStreamDestroy(s);
+}
+
+shs_status check_config(const shs_config& c)
+{
+    if (c.n_layer <= 0 || c.hidden <= 0 || c.n_head <= 0 || c.n_kv_head <= 0 || c.head_dim <= 0 || c.ffn <= 0 || c.vocab <= 0)
+        return fail(SHS_E_INVALID_DATA, "model hyperparameters must be positive");
+    if (c.n_head % c.n_kv_head != 0)
+        return fail(SHS_E_INVALID_DATA, "%d attention heads do not divide into %d KV heads.", c.n_head, c.n_kv_head);
+    if (c.head_dim != 128 || c.n_head / c.n_kv_head > 4)
+        return fail(SHS_E_NOT_SUPPORTED, "the attention kernel needs head_dim 128 and at most 4 query heads per KV head "
+                                         "(got %d and %d)", c.head_dim, c.n_head / c.n_kv_head);
+    if (c.hidden % 32 || c.ffn % 32 || c.rope_dim > c.head_dim || c.rope_dim <= 0 || c.rope_dim % 2)
+        return fail(SHS_E_INVALID_DATA, "hidden and ffn must be multiples of 32 and rope_dim an even number ≤ head_dim");
+    return SHS_OK;
+}
+
+// MinistralModel's constructor (MinistralModel.cs:59-108) over a set of tensor specs.
+shs_status build_model(const shs_config& c, const SpecMap& tm, int device, int initial_capacity, shs_model** out)
+{
+    shs_status st = check_config(c);
+    if (st != SHS_OK) return st;
+    if ((st = select_device(device)) != SHS_OK) return st;
+    shs_model* m = new shs_model();
+    m->cfg = c;
+    m->device = device;
+    auto bail = [&](shs_status s) {
+        std::string keep = g_error;
+        destroy_model(m);
+        g_error = keep;
+        return s;
+    };
+    hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return bail(hip_fail(e, "hipStreamCreate"));
+    m->layers.reserve(c.n_layer);
+
+    const int qdim = c.n_head * c.head_dim, kvdim = c.n_kv_head * c.head_dim;
+    Buf staging;
+    const Spec* t;
+    if ((st = need_tensor(tm, "token_embd.weight", &t)) != SHS_OK) return bail(st);
+    if ((st = check_matrix(t, c.hidden, c.vocab)) != SHS_OK) return bail(st);
+    if ((e = alloc_matrix(m->embd, t->type, c.vocab, c.hidden)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(token_embd)"));
+    if ((e = upload_rows(m->embd, t->src, 0, c.vocab, staging, m->stream)) != hipSuccess) return bail(hip_fail(e, "upload token_embd"));
+    m->where[t->name] = TensorLoc{&m->embd, 0, c.vocab, nullptr, 0};
+    // Shieldstral ties the LM head to token_embd; output.weight is used when present
+    // (MinistralModel.cs:76-78, 250).
+    const Spec* head = tm.get("output.weight");
+    if (head) {
+        if ((st = check_matrix(head, c.hidden, c.vocab)) != SHS_OK) return bail(st);
+        if ((e = alloc_matrix(m->head, head->type, c.vocab, c.hidden)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(output)"));
+        if ((e = upload_rows(m->head, head->src, 0, c.vocab, staging, m->stream)) != hipSuccess) return bail(hip_fail(e, "upload output"));
+        m->tied = false;
+        m->where[head->name] = TensorLoc{&m->head, 0, c.vocab, nullptr, 0};
+    } else {
+        m->head = m->embd;
+        m->tied = true;
+    }
+    if ((st = need_tensor(tm, "output_norm.weight", &t)) != SHS_OK) return bail(st);
+    if ((st = upload_vector(m, t, c.hidden, &m->out_norm)) != SHS_OK) return bail(st);
+
+    m->layers.resize(c.n_layer);
+    for (int l = 0; l < c.n_layer; l++) {
+        Layer& L = m->layers[l];
+        std::string p = "blk." + std::to_string(l) + ".";
+        const Spec *an, *fn, *q, *k, *v, *o, *g, *u, *d;
+        if ((st = need_tensor(tm, p + "attn_norm.weight", &an)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "attn_q.weight", &q)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "attn_k.weight", &k)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "attn_v.weight", &v)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "attn_output.weight", &o)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "ffn_norm.weight", &fn)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "ffn_gate.weight", &g)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "ffn_up.weight", &u)) != SHS_OK) return bail(st);
+        if ((st = need_tensor(tm, p + "ffn_down.weight", &d)) != SHS_OK) return bail(st);
+        if ((st = check_matrix(q, c.hidden, qdim)) != SHS_OK) return bail(st);
+        if ((st = check_matrix(k, c.hidden, kvdim)) != SHS_OK) return bail(st);
+        if ((st = check_matrix(v, c.hidden, kvdim)) != SHS_OK) return bail(st);
+        if ((st = check_matrix(o, qdim, c.hidden)) != SHS_OK) return bail(st);
+        if ((st = check_matrix(g, c.hidden, c.ffn)) != SHS_OK) return bail(st);
+        if ((st = check_matrix(u, c.hidden, c.ffn)) != SHS_OK) return bail(st);
+        if ((st = check_matrix(d, c.ffn, c.hidden)) != SHS_OK) return bail(st);
+        if ((st = upload_vector(m, an, c.hidden, &L.attn_norm)) != SHS_OK) return bail(st);
+        if ((st = upload_vector(m, fn, c.hidden, &L.ffn_norm)) != SHS_OK) return bail(st);
+        if ((st = load_proj(m, L.qkv, {q, k, v}, staging)) != SHS_OK) return bail(st);
+        if ((st = load_proj(m, L.o, {o}, staging)) != SHS_OK) return bail(st);
+        if ((st = load_proj(m, L.gu, {g, u}, staging)) != SHS_OK) return bail(st);
+        if ((st = load_proj(m, L.down, {d}, staging)) != SHS_OK) return bail(st);
+    }
+    rope_freqs(c, m->freqs, m->mscale);
+    if ((st = ensure_kv(m, std::max(1, initial_capacity))) != SHS_OK) return bail(st);
+    if ((st = ensure_rope(m, std::max(512, initial_capacity))) != SHS_OK) return bail(st);
+    *out = m;
+    return SHS_OK;
+}
+
+}  // namespace
+
+extern "C" shs_status shs_open_tensors(const shs_config* cfg, const shs_tensor* tensors, int32_t n_tensors,
+                                       int32_t device, int32_t initial_capacity, shs_model** out)
+{
+    if (!cfg || !out || (!tensors && n_tensors > 0)) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    SpecMap tm;
+    for (int i = 0; i < n_tensors; i++) {
+        const shs_tensor& t = tensors[i];
+        if (!t.name) return fail(SHS_E_INVALID_ARGUMENT, "tensor %d has no name", i);
+        if (!t.data) return fail(SHS_E_INVALID_ARGUMENT, "tensor '%s' has no data", t.name);
+        Spec s;
+        s.name = t.name;
+        s.type = t.type;
+        s.ne0 = t.ne0;
+        s.ne1 = t.ne1 <= 0 ? 1 : t.ne1;
+        s.src = host_src(t.data);
+        tm.byname[s.name] = s;
+    }
+    return build_model(*cfg, tm, device, initial_capacity, out);
+}
+
+extern "C" shs_status shs_open_synthetic(const shs_config* cfg, int32_t weight_type, int32_t embd_type, uint64_t seed,
+                                         int32_t device, int32_t initial_capacity, shs_model** out)
+{
+    if (!cfg || !out) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    const shs_config& c = *cfg;
+    if (c.n_layer <= 0) return fail(SHS_E_INVALID_DATA, "model hyperparameters must be positive");
+    const int64_t qdim = (int64_t)c.n_head * c.head_dim, kvdim = (int64_t)c.n_kv_head * c.head_dim;
+    SpecMap tm;
+    uint64_t id = 0;
+    auto add = [&](const std::string& name, int type, int64_t ne0, int64_t ne1, float mean, float std) {
+        Spec s;
+        s.name = name;
+        s.type = type;
+        s.ne0 = ne0;
+        s.ne1 = ne1;
+        s.src.seed = seed;
+        s.src.id = id++;
+        s.src.mean = mean;
+        s.src.std = std;
+        tm.byname[name] = s;
+    };
+    add("token_embd.weight", embd_type, c.hidden, c.vocab, 0.0f, 0.02f);
+    add("output_norm.weight", SHS_F32, c.hidden, 1, 1.0f, 0.1f);
+    for (int l = 0; l < c.n_layer; l++) {
+        std::string p = "blk." + std::to_string(l) + ".";
+        add(p + "attn_norm.weight", SHS_F32, c.hidden, 1, 1.0f, 0.1f);
+        add(p + "attn_q.weight", weight_type, c.hidden, qdim, 0.0f, 0.02f);
+        add(p + "attn_k.weight", weight_type, c.hidden, kvdim, 0.0f, 0.02f);
+        add(p + "attn_v.weight", weight_type, c.hidden, kvdim, 0.0f, 0.02f);
+        add(p + "attn_output.weight", weight_type, qdim, c.hidden, 0.0f, 0.02f);
+        add(p + "ffn_norm.weight", SHS_F32, c.hidden, 1, 1.0f, 0.1f);
+        add(p + "ffn_gate.weight", weight_type, c.hidden, c.ffn, 0.0f, 0.02f);
+        add(p + "ffn_up.weight", weight_type, c.hidden, c.ffn, 0.0f, 0.02f);
+        add(p + "ffn_down.weight", weight_type, c.ffn, c.hidden, 0.0f, 0.02f);
+    }
+    return build_model(c, tm, device, initial_capacity, out);
+}
+
+extern "C" shs_status shs_tensor_download(shs_model* m, const char* name, void* dst, size_t bytes)
+{
+    if (!m || !name || !dst) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    auto it = m->where.find(name);
+    if (it == m->where.end()) return fail(SHS_E_KEY_NOT_FOUND, "tensor '%s' is not part of this model", name);
+    const TensorLoc& loc = it->second;
+    HIP_TRY(hipSetDevice(m->device));
+    if (loc.vec) {
+        if (bytes != sizeof(float) * (size_t)loc.n)
+            return fail(SHS_E_INVALID_ARGUMENT, "'%s' is %d fp32 values; buffer holds %zu bytes", name, loc.n, bytes);
+        HIP_TRY(hipMemcpy(dst, loc.vec, bytes, hipMemcpyDeviceToHost));
+        return SHS_OK;
+    }
+    size_t need = (size_t)loc.rows * (size_t)row_bytes(loc.mat->type, loc.mat->cols);
+    if (bytes != need) return fail(SHS_E_INVALID_ARGUMENT, "'%s' is %zu bytes; buffer holds %zu", name, need, bytes);
+    Buf tmp;
+    HIP_TRY(tmp.ensure(need));
+    HIP_TRY(launch_unpack_native(*loc.mat, loc.row0, loc.rows, tmp.as<uint8_t>(), m->stream));
+    HIP_TRY(hipMemcpyAsync(dst, tmp.p, need, hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+extern "C" void shs_close(shs_model* m) { destroy_model(m); }
+
+extern "C" shs_status shs_get_config(const shs_model* m, shs_config* out)
+{
+    if (!m || !out) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    *out = m->cfg;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_kv_reset(shs_model* m)
+{
+    if (!m) return fail(SHS_E_INVALID_ARGUMENT, "null model");
+    m->len = 0;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_kv_length(const shs_model* m, int32_t* n)
+{
+    if (!m || !n) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    *n = m->len;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_kv_capacity(const shs_model* m, int32_t* n)
+{
+    if (!m || !n) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    *n = m->cap;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_kv_snapshot(shs_model* m, int32_t length, float* dst, size_t n_floats)
+{
+    if (!m || (!dst && length > 0)) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (length < 0 || length > m->len)
+        return fail(SHS_E_OUT_OF_RANGE, "only %d positions are cached; cannot snapshot %d", m->len, length);
+    size_t hd = m->cfg.head_dim, rows = (size_t)m->cfg.n_layer * m->cfg.n_kv_head;
+    size_t per = rows * length * hd;
+    if (n_floats != 2 * per)
+        return fail(SHS_E_INVALID_ARGUMENT, "snapshot of %d positions holds %zu floats, buffer has %zu", length, 2 * per, n_floats);
+    if (length == 0) return SHS_OK;
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipMemcpy2DAsync(dst, length * hd * 4, m->kc, m->cap * hd * 4, length * hd * 4, rows, hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipMemcpy2DAsync(dst + per, length * hd * 4, m->vc, m->cap * hd * 4, length * hd * 4, rows, hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_kv_restore(shs_model* m, const float* src, size_t n_floats, int32_t length)
+{
+    if (!m || (!src && length > 0)) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (length < 0) return fail(SHS_E_OUT_OF_RANGE, "negative length");
+    size_t hd = m->cfg.head_dim, rows = (size_t)m->cfg.n_layer * m->cfg.n_kv_head;
+    size_t per = rows * length * hd;
+    if (n_floats != 2 * per)
+        return fail(SHS_E_INVALID_ARGUMENT, "Snapshot holds %zu floats; %d positions need %zu.", n_floats, length, 2 * per);
+    HIP_TRY(hipSetDevice(m->device));
+    shs_status st = ensure_kv(m, length);
+    if (st != SHS_OK) return st;
+    if (length > 0) {
+        HIP_TRY(hipMemcpy2DAsync(m->kc, m->cap * hd * 4, src, length * hd * 4, length * hd * 4, rows, hipMemcpyHostToDevice, m->stream));
+        HIP_TRY(hipMemcpy2DAsync(m->vc, m->cap * hd * 4, src + per, length * hd * 4, length * hd * 4, rows, hipMemcpyHostToDevice, m->stream));
+        HIP_TRY(hipStreamSynchronize(m->stream));
+    }
+    m->len = length;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_set_capture(shs_model* m, shs_capture_fn fn, void* user)
+{
+    if (!m) return fail(SHS_E_INVALID_ARGUMENT, "null model");
+    m->cap_fn = fn;
+    m->cap_user = user;
+    return SHS_OK;
+}
+
+// ------------------------------------------------------------- forward
+
+namespace {
+
+struct Capture {
+    shs_model* m;
+    std::vector<float> host;
+    shs_status observe(const char* name, const float* dev, int ld, int rows, int cols)
+    {
+        if (!m->cap_fn) return SHS_OK;
+        host.resize((size_t)rows * cols);
+        HIP_TRY(hipStreamSynchronize(m->stream));
+        HIP_TRY(hipMemcpy2D(host.data(), cols * sizeof(float), dev, ld * sizeof(float), cols * sizeof(float), rows,
+                            hipMemcpyDeviceToHost));
+        m->cap_fn(name, host.data(), rows, cols, m->cap_user);
+        return SHS_OK;
+    }
+};
+
+double gemm_ops(int T, const DevMatrix& w) { return 2.0 * T * (double)w.rows * w.cols; }
+
+shs_status run_proj(shs_model* m, const Proj& p, const ActQ8& a, float* y, int ldy, int mode)
+{
+    for (size_t i = 0; i < p.parts.size(); i++) {
+        Timed tm(m->prof, "gemm", gemm_ops(a.T, p.parts[i]), m->stream);
+        HIP_TRY(launch_gemm(p.parts[i], a, y + p.col0[i], ldy, mode, m->stream));
+    }
+    return SHS_OK;
+}
+
+// Buffers for a pass over T tokens.
+shs_status ensure_work(shs_model* m, int T)
+{
+    const shs_config& c = m->cfg;
+    size_t qdim = (size_t)c.n_head * c.head_dim, kvdim = (size_t)c.n_kv_head * c.head_dim;
+    HIP_TRY(m->h.ensure(sizeof(float) * T * c.hidden));
+    HIP_TRY(m->qkv.ensure(sizeof(float) * T * (qdim + 2 * kvdim)));
+    HIP_TRY(m->ctx.ensure(sizeof(float) * T * qdim));
+    HIP_TRY(m->gu.ensure(sizeof(float) * T * 2 * (size_t)c.ffn));
+    HIP_TRY(m->tmp.ensure(sizeof(float) * T * std::max<size_t>(c.hidden, c.ffn)));
+    HIP_TRY(m->normed.ensure(sizeof(float) * T * (size_t)c.hidden));
+    HIP_TRY(m->tokens.ensure(sizeof(int32_t) * T));
+    HIP_TRY(m->pos.ensure(sizeof(int32_t) * T));
+    return SHS_OK;
+}
+
+// The decoder layers over the T tokens in m->h. Keys and values for token t go to cache
+// slot slot0 + t of (kc, vc) whose per-head stride is cap positions; attention runs over
+// the given work items. cancel is polled between layers.
+shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap, int slot0, int l_begin, int l_end,
+                      const AttnItem* items_dev, int n_items, const volatile int32_t* cancel, bool per_layer_kv)
+{
+    const shs_config& c = m->cfg;
+    const int hidden = c.hidden, qdim = c.n_head * c.head_dim, kvdim = c.n_kv_head * c.head_dim;
+    const int ldqkv = qdim + 2 * kvdim;
+    float* h = m->h.as<float>();
+    float* qkv = m->qkv.as<float>();
+    float* ctx = m->ctx.as<float>();
+    float* gu = m->gu.as<float>();
+    float* tmp = m->tmp.as<float>();
+    const bool cap_on = m->cap_fn != nullptr;
+    float* normed = cap_on ? m->normed.as<float>() : nullptr;
+    Capture cp{m, {}};
+    char name[96];
+    const float scale = 1.0f / sqrtf((float)c.head_dim);
+    ActQ8 a;
+    HIP_TRY(m->act.ensure(T, std::max(std::max(hidden, qdim), c.ffn), &a));
+
+    for (int l = l_begin; l < l_end; l++) {
+        if (cancel && *cancel) {
+            (void)hipStreamSynchronize(m->stream);
+            return fail(SHS_E_CANCELLED, "The operation was canceled.");
+        }
+        const Layer& L = m->layers[l];
+        float* kc = per_layer_kv ? kc_all + kv_layer_floats(m, cap) * l : kc_all;
+        float* vc = per_layer_kv ? vc_all + kv_layer_floats(m, cap) * l : vc_all;
+
+        ActQ8 ah = a;
+        ah.K = hidden;
+        ah.B = hidden / 32;
+        {
+            Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
+            HIP_TRY(launch_rmsnorm_quant(h, hidden, L.attn_norm, c.rms_eps, hidden, ah, normed, m->stream));
+        }
+        snprintf(name, sizeof name, "blk.%d.attn_norm", l);
+        if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
+
+        if (run_proj(m, L.qkv, ah, qkv, ldqkv, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+        {
+            Timed tm(m->prof, "rope_store", 0, m->stream);
+            HIP_TRY(launch_rope_store(qkv, ldqkv, T, c.n_head, c.n_kv_head, c.head_dim, m->pos.as<int32_t>(),
+                                      m->cos_tab.as<float>(), m->sin_tab.as<float>(), m->qscale_tab.as<float>(),
+                                      c.rope_dim / 2, kc, vc, cap, slot0, m->stream));
+        }
+        if (cap_on) {
+            snprintf(name, sizeof name, "blk.%d.q_rope", l);
+            if (cp.observe(name, qkv, ldqkv, T, qdim) != SHS_OK) return SHS_E_DEVICE;
+            snprintf(name, sizeof name, "blk.%d.k_rope", l);
+            if (cp.observe(name, qkv + qdim, ldqkv, T, kvdim) != SHS_OK) return SHS_E_DEVICE;
+            snprintf(name, sizeof name, "blk.%d.v", l);
+            if (cp.observe(name, qkv + qdim + kvdim, ldqkv, T, kvdim) != SHS_OK) return SHS_E_DEVICE;
+        }
+        {
+            Timed tm(m->prof, "attention", 0, m->stream);
+            HIP_TRY(launch_attention(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, c.head_dim,
+                                     scale, ctx, qdim, m->stream));
+        }
+        snprintf(name, sizeof name, "blk.%d.attn_weighted", l);
+        if (cap_on && cp.observe(name, ctx, qdim, T, qdim) != SHS_OK) return SHS_E_DEVICE;
+
+        ActQ8 ac = a;
+        ac.K = qdim;
+        ac.B = qdim / 32;
+        {
+            Timed tm(m->prof, "quant_act", 0, m->stream);
+            HIP_TRY(launch_quant_act(ctx, qdim, ac, 0, m->stream));
+        }
+        if (cap_on) {
+            if (run_proj(m, L.o, ac, tmp, hidden, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+            snprintf(name, sizeof name, "blk.%d.attn_out", l);
+            if (cp.observe(name, tmp, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
+            HIP_TRY(launch_add_inplace(h, tmp, (size_t)T * hidden, m->stream));
+            snprintf(name, sizeof name, "blk.%d.post_attn", l);
+            if (cp.observe(name, h, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
+        } else {
+            if (run_proj(m, L.o, ac, h, hidden, GEMM_ADD) != SHS_OK) return SHS_E_DEVICE;
+        }
+
+        {
+            Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
+            HIP_TRY(launch_rmsnorm_quant(h, hidden, L.ffn_norm, c.rms_eps, hidden, ah, normed, m->stream));
+        }
+        snprintf(name, sizeof name, "blk.%d.ffn_norm", l);
+        if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
+
+        if (run_proj(m, L.gu, ah, gu, 2 * c.ffn, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+        ActQ8 af = a;
+        af.K = c.ffn;
+        af.B = c.ffn / 32;
+        {
+            Timed tm(m->prof, "swiglu_quant", 0, m->stream);
+            HIP_TRY(launch_swiglu_quant(gu, 2 * c.ffn, c.ffn, af, nullptr, m->stream));
+        }
+        if (cap_on) {
+            if (run_proj(m, L.down, af, tmp, hidden, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+            snprintf(name, sizeof name, "blk.%d.ffn_out", l);
+            if (cp.observe(name, tmp, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
+            HIP_TRY(launch_add_inplace(h, tmp, (size_t)T * hidden, m->stream));
+            snprintf(name, sizeof name, "blk.%d.output", l);
+            if (cp.observe(name, h, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
+        } else {
+            if (run_proj(m, L.down, af, h, hidden, GEMM_ADD) != SHS_OK) return SHS_E_DEVICE;
+        }
+    }
+    return SHS_OK;
+}
+
+// Final RMSNorm of the rows `rows` of h, then the head: selected rows or the full vocab.
+shs_status run_head(shs_model* m, const std::vector<int32_t>& rows, int head_mode, const int32_t* ids_dev, int n_ids,
+                    float* logits_dev)
+{
+    const shs_config& c = m->cfg;
+    const int n = (int)rows.size();
+    HIP_TRY(m->lastidx.ensure(sizeof(int32_t) * n));
+    HIP_TRY(m->last_rows.ensure(sizeof(float) * (size_t)n * c.hidden));
+    HIP_TRY(m->normed.ensure(sizeof(float) * (size_t)std::max(n, 1) * c.hidden));
+    HIP_TRY(hipMemcpyAsync(m->lastidx.p, rows.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(launch_gather_rows(m->h.as<float>(), c.hidden, m->lastidx.as<int32_t>(), n, c.hidden, m->last_rows.as<float>(),
+                               c.hidden, m->stream));
+    ActQ8 a;
+    HIP_TRY(m->act.ensure(n, c.hidden, &a));
+    float* normed = m->cap_fn ? m->normed.as<float>() : nullptr;
+    {
+        Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
+        HIP_TRY(launch_rmsnorm_quant(m->last_rows.as<float>(), c.hidden, m->out_norm, c.rms_eps, c.hidden, a, normed,
+                                     m->stream));
+    }
+    Capture cp{m, {}};
+    if (m->cap_fn && cp.observe("final_norm", normed, c.hidden, n, c.hidden) != SHS_OK) return SHS_E_DEVICE;
+    if (head_mode == 1) {
+        Timed tm(m->prof, "gemv", 2.0 * n * n_ids * c.hidden, m->stream);
+        HIP_TRY(launch_gemv_rows(m->head, a, ids_dev, n_ids, logits_dev, m->stream));
+    } else {
+        Timed tm(m->prof, "gemm_head", gemm_ops(n, m->head), m->stream);
+        HIP_TRY(launch_gemm(m->head, a, logits_dev, c.vocab, GEMM_STORE, m->stream));
+    }
+    return SHS_OK;
+}
+
+shs_status check_ids(const int32_t* ids, int n, int limit, const char* what)
+{
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= limit)
+            return fail(SHS_E_OUT_OF_RANGE, "%s %d is outside the %d-entry table.", what, ids[i], limit);
+    return SHS_OK;
+}
+
+std::vector<AttnItem> causal_items(int q_begin, int n, int key_start, int pos0)
+{
+    std::vector<AttnItem> v;
+    for (int k = 0; k * 32 < n; k++) v.push_back({q_begin + 32 * k, std::min(32, n - 32 * k), key_start, pos0 + 32 * k});
+    return v;
+}
+
+}  // namespace
+
+extern "C" shs_status shs_forward(shs_model* m, const int32_t* tokens, int32_t n, int32_t head_mode,
+                                  const int32_t* vocab_ids, int32_t n_ids, float* logits_out,
+                                  const volatile int32_t* cancel)
+{
+    if (!m || !tokens) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (n <= 0) return fail(SHS_E_INVALID_ARGUMENT, "No tokens to forward.");
+    if (head_mode < 0 || head_mode > 2) return fail(SHS_E_INVALID_ARGUMENT, "head_mode must be 0, 1 or 2");
+    if (head_mode == 1 && (!vocab_ids || n_ids <= 0 || !logits_out))
+        return fail(SHS_E_INVALID_ARGUMENT, "selected-rows head needs vocab_ids and logits_out");
+    if (head_mode == 2 && !logits_out) return fail(SHS_E_INVALID_ARGUMENT, "full head needs logits_out");
+    const shs_config& c = m->cfg;
+    shs_status st;
+    if ((st = check_ids(tokens, n, c.vocab, "Token id")) != SHS_OK) return st;
+    if (head_mode == 1 && (st = check_ids(vocab_ids, n_ids, c.vocab, "Row")) != SHS_OK) return st;
+    HIP_TRY(hipSetDevice(m->device));
+    const int start = m->len;
+    if ((st = ensure_kv(m, start + n)) != SHS_OK) return st;
+    if ((st = ensure_rope(m, start + n)) != SHS_OK) return st;
+    if ((st = ensure_work(m, n)) != SHS_OK) return st;
+
+    std::vector<int32_t> pos(n);
+    for (int t = 0; t < n; t++) pos[t] = start + t;
+    std::vector<AttnItem> items = causal_items(0, n, 0, start);
+    HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
+    HIP_TRY(hipMemcpyAsync(m->tokens.p, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
+    if (head_mode == 1) {
+        HIP_TRY(m->ids.ensure(sizeof(int32_t) * n_ids));
+        HIP_TRY(hipMemcpyAsync(m->ids.p, vocab_ids, sizeof(int32_t) * n_ids, hipMemcpyHostToDevice, m->stream));
+    }
+    {
+        Timed tm(m->prof, "embed", 0, m->stream);
+        HIP_TRY(launch_embed(m->embd, m->tokens.as<int32_t>(), n, m->h.as<float>(), c.hidden, m->stream));
+    }
+    Capture cp{m, {}};
+    if (m->cap_fn && cp.observe("embeddings", m->h.as<float>(), c.hidden, n, c.hidden) != SHS_OK) return SHS_E_DEVICE;
+
+    st = run_layers(m, n, m->kc, m->vc, m->cap, start, 0, c.n_layer, m->items.as<AttnItem>(), (int)items.size(), cancel, true);
+    if (st != SHS_OK) {
+        (void)hipStreamSynchronize(m->stream);
+        return st;
+    }
+    if (head_mode != 0) {
+        int n_out = head_mode == 1 ? n_ids : c.vocab;
+        HIP_TRY(m->logits.ensure(sizeof(float) * n_out));
+        if ((st = run_head(m, {n - 1}, head_mode, m->ids.as<int32_t>(), n_ids, m->logits.as<float>())) != SHS_OK) return st;
+        HIP_TRY(hipMemcpyAsync(logits_out, m->logits.p, sizeof(float) * n_out, hipMemcpyDeviceToHost, m->stream));
+    }
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    if (head_mode == 2 && m->cap_fn) m->cap_fn("logits", logits_out, 1, c.vocab, m->cap_user);
+    // KvCache.Advance only after a complete pass (MinistralModel.cs:240).
+    m->len = start + n;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_forward_batch(shs_model* m, const int32_t* tokens, const int32_t* cu, int32_t n_seq,
+                                        const int32_t* vocab_ids, int32_t n_ids, float* logits_out)
+{
+    if (!m || !tokens || !cu || !vocab_ids || !logits_out) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (n_seq <= 0 || n_ids <= 0) return fail(SHS_E_INVALID_ARGUMENT, "need at least one sequence and one vocab id");
+    if (cu[0] != 0) return fail(SHS_E_INVALID_ARGUMENT, "cu_seqlens[0] must be 0");
+    for (int s = 0; s < n_seq; s++)
+        if (cu[s + 1] <= cu[s]) return fail(SHS_E_INVALID_ARGUMENT, "sequence %d is empty or cu_seqlens is not increasing", s);
+    const int T = cu[n_seq];
+    const shs_config& c = m->cfg;
+    shs_status st;
+    if ((st = check_ids(tokens, T, c.vocab, "Token id")) != SHS_OK) return st;
+    if ((st = check_ids(vocab_ids, n_ids, c.vocab, "Row")) != SHS_OK) return st;
+    HIP_TRY(hipSetDevice(m->device));
+    int longest = 0;
+    for (int s = 0; s < n_seq; s++) longest = std::max(longest, cu[s + 1] - cu[s]);
+    if ((st = ensure_rope(m, longest)) != SHS_OK) return st;
+    if ((st = ensure_work(m, T)) != SHS_OK) return st;
+    // One layer's worth of packed K/V, reused layer after layer.
+    const int cap = T;
+    const size_t kvf = (size_t)c.n_kv_head * cap * c.head_dim;
+    HIP_TRY(m->bkc.ensure(sizeof(float) * kvf));
+    HIP_TRY(m->bvc.ensure(sizeof(float) * kvf));
+
+    std::vector<int32_t> pos(T);
+    std::vector<AttnItem> items;
+    for (int s = 0; s < n_seq; s++) {
+        for (int t = cu[s]; t < cu[s + 1]; t++) pos[t] = t - cu[s];
+        auto v = causal_items(cu[s], cu[s + 1] - cu[s], cu[s], 0);
+        items.insert(items.end(), v.begin(), v.end());
+    }
+    // The kernel takes items from the back: put the longest key ranges there.
+    std::stable_sort(items.begin(), items.end(),
+                     [](const AttnItem& x, const AttnItem& y) { return x.pos0 + x.q_count < y.pos0 + y.q_count; });
+    HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
+    HIP_TRY(m->ids.ensure(sizeof(int32_t) * n_ids));
+    HIP_TRY(hipMemcpyAsync(m->tokens.p, tokens, sizeof(int32_t) * T, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * T, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->ids.p, vocab_ids, sizeof(int32_t) * n_ids, hipMemcpyHostToDevice, m->stream));
+    {
+        Timed tm(m->prof, "embed", 0, m->stream);
+        HIP_TRY(launch_embed(m->embd, m->tokens.as<int32_t>(), T, m->h.as<float>(), c.hidden, m->stream));
+    }
+    st = run_layers(m, T, m->bkc.as<float>(), m->bvc.as<float>(), cap, 0, 0, c.n_layer, m->items.as<AttnItem>(),
+                    (int)items.size(), nullptr, false);
+    if (st != SHS_OK) {
+        (void)hipStreamSynchronize(m->stream);
+        return st;
+    }
+    std::vector<int32_t> last(n_seq);
+    for (int s = 0; s < n_seq; s++) last[s] = cu[s + 1] - 1;
+    HIP_TRY(m->logits.ensure(sizeof(float) * (size_t)n_seq * n_ids));
+    if ((st = run_head(m, last, 1, m->ids.as<int32_t>(), n_ids, m->logits.as<float>())) != SHS_OK) return st;
+    HIP_TRY(hipMemcpyAsync(logits_out, m->logits.p, sizeof(float) * (size_t)n_seq * n_ids, hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_layer_forward(shs_model* m, int32_t layer, const float* x, int32_t n, float* y)
+{
+    if (!m || !x || !y) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (layer < 0 || layer >= m->cfg.n_layer) return fail(SHS_E_OUT_OF_RANGE, "layer %d does not exist", layer);
+    if (n <= 0) return fail(SHS_E_INVALID_ARGUMENT, "No tokens to forward.");
+    const shs_config& c = m->cfg;
+    HIP_TRY(hipSetDevice(m->device));
+    shs_status st;
+    if ((st = ensure_kv(m, n)) != SHS_OK) return st;
+    if ((st = ensure_rope(m, n)) != SHS_OK) return st;
+    if ((st = ensure_work(m, n)) != SHS_OK) return st;
+    std::vector<int32_t> pos(n);
+    for (int t = 0; t < n; t++) pos[t] = t;
+    std::vector<AttnItem> items = causal_items(0, n, 0, 0);
+    HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
+    HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->h.p, x, sizeof(float) * (size_t)n * c.hidden, hipMemcpyHostToDevice, m->stream));
+    m->len = 0;
+    st = run_layers(m, n, m->kc, m->vc, m->cap, 0, layer, layer + 1, m->items.as<AttnItem>(), (int)items.size(), nullptr, true);
+    (void)hipStreamSynchronize(m->stream);
+    if (st != SHS_OK) return st;
+    HIP_TRY(hipMemcpy(y, m->h.p, sizeof(float) * (size_t)n * c.hidden, hipMemcpyDeviceToHost));
+    m->len = 0;
+    return SHS_OK;
+}
+
+// --------------------------------------------------------------- profiling
+
+extern "C" shs_status shs_profile_enable(shs_model* m, int32_t enable)
+{
+    if (!m) return fail(SHS_E_INVALID_ARGUMENT, "null model");
+    m->prof.on = enable != 0;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_profile_read(shs_model* m, const char* cls, int64_t* launches, double* total_ms, double* total_ops)
+{
+    if (!m || !cls) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    (void)hipSetDevice(m->device);
+    m->prof.collect();
+    auto it = m->prof.totals.find(cls);
+    int64_t n = 0;
+    double ms = 0, ops = 0;
+    if (it != m->prof.totals.end()) {
+        n = it->second.first;
+        ms = it->second.second.first;
+        ops = it->second.second.second;
+    }
+    if (launches) *launches = n;
+    if (total_ms) *total_ms = ms;
+    if (total_ops) *total_ops = ops;
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_profile_reset(shs_model* m)
+{
+    if (!m) return fail(SHS_E_INVALID_ARGUMENT, "null model");
+    (void)hipSetDevice(m->device);
+    m->prof.collect();
+    m->prof.totals.clear();
+    return SHS_OK;
+}
+
+// ------------------------------------------------------- quantized matmul
+
+extern "C" shs_status shs_matrix_create(int32_t type, int32_t rows, int32_t cols, const void* data, int32_t device,
+                                        shs_matrix** out)
+{
+    if (!data || !out) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (!type_supported(type))
+        return fail(SHS_E_NOT_SUPPORTED, "%s has no integer GEMM kernel.", type_name(type));
+    if (rows <= 0 || cols <= 0 || cols % 32)
+        return fail(SHS_E_INVALID_ARGUMENT, "a %d x %d matrix: rows must be positive and cols a positive multiple of 32",
+                    rows, cols);
+    shs_status st = select_device(device);
+    if (st != SHS_OK) return st;
+    shs_matrix* m = new shs_matrix();
+    m->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = alloc_matrix(m->w, type, rows, cols);
+    Buf staging;
+    if (e == hipSuccess) e = upload_rows(m->w, host_src(data), 0, rows, staging, m->stream);
+    if (e != hipSuccess) {
+        shs_matrix_free(m);
+        return hip_fail(e, "shs_matrix_create");
+    }
+    *out = m;
+    return SHS_OK;
+}
+
+extern "C" void shs_matrix_free(shs_matrix* m)
+{
+    if (!m) return;
+    (void)hipSetDevice(m->device);
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    free_matrix(m->w);
+    hipStream_t s = m->stream;
+    delete m;
+    if (s) (void)hipStreamDestroy(s);
+}
+
+static shs_status matmul_common(shs_matrix* m, const float* x, int T, int semantics, ActQ8* a, bool x_on_device)
+{
+    if (!m || !x) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (T <= 0) return fail(SHS_E_INVALID_ARGUMENT, "tokens must be positive");
+    if (semantics != 0 && semantics != 1) return fail(SHS_E_INVALID_ARGUMENT, "semantics must be 0 or 1");
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(m->act.ensure(T, m->w.cols, a));
+    const float* xd = x;
+    if (!x_on_device) {
+        HIP_TRY(m->x.ensure(sizeof(float) * (size_t)T * m->w.cols));
+        HIP_TRY(hipMemcpyAsync(m->x.p, x, sizeof(float) * (size_t)T * m->w.cols, hipMemcpyHostToDevice, m->stream));
+        xd = m->x.as<float>();
+    }
+    HIP_TRY(launch_quant_act(xd, m->w.cols, *a, semantics, m->stream));
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_matmul(shs_matrix* m, const float* x, int32_t T, float* y, int32_t semantics)
+{
+    if (!y) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    ActQ8 a;
+    shs_status st = matmul_common(m, x, T, semantics, &a, false);
+    if (st != SHS_OK) return st;
+    HIP_TRY(m->y.ensure(sizeof(float) * (size_t)T * m->w.rows));
+    HIP_TRY(launch_gemm(m->w, a, m->y.as<float>(), m->w.rows, GEMM_STORE, m->stream));
+    HIP_TRY(hipMemcpyAsync(y, m->y.p, sizeof(float) * (size_t)T * m->w.rows, hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_matmul_rows(shs_matrix* m, const int32_t* ids, int32_t n_ids, const float* x, int32_t T, float* y)
+{
+    if (!ids || !y || n_ids <= 0) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (!m) return fail(SHS_E_INVALID_ARGUMENT, "null matrix");
+    for (int i = 0; i < n_ids; i++)
+        if (ids[i] < 0 || ids[i] >= m->w.rows)
+            return fail(SHS_E_OUT_OF_RANGE, "Row %d is outside the matrix's %d rows.", ids[i], m->w.rows);
+    ActQ8 a;
+    shs_status st = matmul_common(m, x, T, 0, &a, false);
+    if (st != SHS_OK) return st;
+    HIP_TRY(m->ids.ensure(sizeof(int32_t) * n_ids));
+    HIP_TRY(m->y.ensure(sizeof(float) * (size_t)T * n_ids));
+    HIP_TRY(hipMemcpyAsync(m->ids.p, ids, sizeof(int32_t) * n_ids, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(launch_gemv_rows(m->w, a, m->ids.as<int32_t>(), n_ids, m->y.as<float>(), m->stream));
+    HIP_TRY(hipMemcpyAsync(y, m->y.p, sizeof(float) * (size_t)T * n_ids, hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_matmul_block_sums(shs_matrix* m, const float* x, int32_t T, int32_t* out)
+{
+    if (!out) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    ActQ8 a;
+    shs_status st = matmul_common(m, x, T, 0, &a, false);
+    if (st != SHS_OK) return st;
+    size_t n = (size_t)T * m->w.rows * m->w.blocks;
+    HIP_TRY(m->sums.ensure(sizeof(int32_t) * n));
+    HIP_TRY(launch_gemm_block_sums(m->w, a, m->sums.as<int32_t>(), m->stream));
+    HIP_TRY(hipMemcpyAsync(out, m->sums.p, sizeof(int32_t) * n, hipMemcpyDeviceToHost, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_matmul_device(shs_matrix* m, const float* x_dev, int32_t T, float* y_dev)
+{
+    if (!y_dev) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    ActQ8 a;
+    shs_status st = matmul_common(m, x_dev, T, 0, &a, true);
+    if (st != SHS_OK) return st;
+    HIP_TRY(launch_gemm(m->w, a, y_dev, m->w.rows, GEMM_STORE, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+// Error hook for the GGUF reader (shs_gguf.cpp), which shares this thread-local message.
+extern "C" __attribute__((visibility("hidden"))) shs_status shs_gguf_fail(shs_status code, const char* msg)
+{
+    g_error = msg;
+    return code;
+}

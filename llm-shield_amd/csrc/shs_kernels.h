@@ -1,0 +1,88 @@
+// Internal interface between the host runtime (shs_api.cpp) and the gfx950 kernels
+// (shs_kernels.hip). Device layouts are described once here.
+//
+// Repacked weight matrix (rows padded to a multiple of 32, B = cols/32 blocks):
+//   record (tile, b) for 32 consecutive rows × one 32-wide block:
+//     qs  [tiles][B][32 rows][QSB]  QSB = 16 (4/5-bit types; GGUF nibble order kept)
+//                                   QSB = 32 (Q8_0; bytes permuted like activations)
+//     qh  [tiles][B][32 rows] u32   fifth bits (Q5_0/Q5_1), GGUF bit order kept
+//     d   [tiles][B][32 rows] f32   block scale, fp16 widened exactly
+//     m   [tiles][B][32 rows] f32   block min (Q4_1/Q5_1)
+// Quantized activations (T padded to Tpad, a multiple of 32):
+//     q   [Tpad/32][B][32 tokens][32 B]  int8, each block stored in the order
+//                                        [0..7, 16..23 | 8..15, 24..31] so MFMA lane half h
+//                                        reads bytes 16h..16h+15 (matches the weight nibbles)
+//     d   [B][Tpad] f32   scale max|x|/127
+//     ds  [B][Tpad] f32   RN(d·float(Σq)) — the offset types' second factor
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace shs {
+
+enum { SHS_TYPE_F32 = 0, SHS_TYPE_F16 = 1, SHS_TYPE_Q4_0 = 2, SHS_TYPE_Q4_1 = 3,
+       SHS_TYPE_Q5_0 = 6, SHS_TYPE_Q5_1 = 7, SHS_TYPE_Q8_0 = 8 };
+
+struct DevMatrix {
+    int type = -1, rows = 0, cols = 0, blocks = 0, tiles = 0;
+    uint8_t* qs = nullptr;
+    uint32_t* qh = nullptr;
+    float* d = nullptr;
+    float* m = nullptr;
+};
+
+struct ActQ8 {
+    int T = 0, Tpad = 0, K = 0, B = 0;
+    int8_t* q = nullptr;
+    float* d = nullptr;
+    float* ds = nullptr;
+};
+
+// Work item of the attention kernel: queries [q_start, q_start+q_count) of one
+// sequence, whose first query sits at position pos0 and whose keys live at cache
+// index key_start + p for p in [0, pos0 + q_count).
+struct AttnItem {
+    int q_start, q_count, key_start, pos0;
+};
+
+enum GemmMode { GEMM_STORE = 0, GEMM_ADD = 1 };
+
+int qs_bytes(int type);
+bool type_supported(int type);
+bool type_has_offset(int type);
+bool type_has_qh(int type);
+
+// All launchers return hipError_t of the launch.
+hipError_t launch_repack(const DevMatrix& m, const uint8_t* native, int row0, int nrows, hipStream_t s);
+hipError_t launch_quant_act(const float* x, int ldx, const ActQ8& a, int semantics, hipStream_t s);
+hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float eps, int n, const ActQ8& a,
+                                float* y_opt, hipStream_t s);
+hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& a, float* y_opt, hipStream_t s);
+hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s);
+hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* out, hipStream_t s);
+hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* row_ids, int n_ids, float* y,
+                            hipStream_t s);
+hipError_t launch_embed(const DevMatrix& table, const int32_t* ids, int n, float* h, int ldh, hipStream_t s);
+hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv_head, int head_dim,
+                             const int32_t* pos, const float* cos_tab, const float* sin_tab,
+                             const float* qscale_tab, int half, float* kc, float* vc, int cap,
+                             int kv_slot0, hipStream_t s);
+hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap,
+                            const AttnItem* items, int n_items, int n_head, int n_kv_head, int head_dim,
+                            float scale, float* ctx, int ldc, hipStream_t s);
+hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s);
+hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);
+hipError_t launch_add_inplace(float* a, const float* b, size_t n, hipStream_t s);
+hipError_t launch_gather_rows(const float* src, int lds, const int32_t* rows, int n, int cols, float* dst, int ldd,
+                              hipStream_t s);
+
+// Synthetic random-init weights: N(mean, std) from a counter-based generator keyed by
+// (seed, tensor id, element), quantized with the ggml block rules into native layout.
+hipError_t launch_synth_native(int type, uint64_t seed, uint64_t tensor_id, int rows, int cols, float mean, float std,
+                               uint8_t* native, hipStream_t s);
+hipError_t launch_synth_f32(uint64_t seed, uint64_t tensor_id, int64_t n, float mean, float std, float* out,
+                            hipStream_t s);
+// Inverse of launch_repack: rows [0, rows) back to native GGUF blocks.
+hipError_t launch_unpack_native(const DevMatrix& m, int row0, int nrows, uint8_t* native, hipStream_t s);
+
+}  // namespace shs

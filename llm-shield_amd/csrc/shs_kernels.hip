@@ -1,0 +1,1034 @@
+// gfx950 kernels of the Shieldstral prefill path. Device layouts: shs_kernels.h.
+//
+// Numerics follow the reference bit for bit where it is integer or a single IEEE op:
+// activation quantization (IntegerGemm.cs:97-138), the exact int32 block sums and the
+// serial per-block epilogue acc = fma(float(I_b), RN(d_w·d_a), acc) (IntegerGemm.cs:
+// 376-418), RMSNorm's accumulation order (Kernels.cs:26-61) and RoPE's rotation
+// (Rope.cs:112-135). The file is compiled with -ffp-contract=off; every fma is explicit.
+#include "shs_kernels.h"
+
+#include <math.h>
+
+namespace shs {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+int qs_bytes(int type) { return type == SHS_TYPE_Q8_0 ? 32 : 16; }
+bool type_supported(int t) { return t == 2 || t == 3 || t == 6 || t == 7 || t == 8; }
+bool type_has_offset(int t) { return t == 3 || t == 7; }
+bool type_has_qh(int t) { return t == 6 || t == 7; }
+
+// Exact fp16 → fp32 for every bit pattern (IntegerGemm.HalfToSingle, IntegerGemm.cs:235-245).
+__device__ inline float half_bits_to_float(uint32_t h)
+{
+    uint32_t sign = (h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do { man <<= 1; e++; } while ((man & 0x400u) == 0);
+            man &= 0x3FFu;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 0x1F) {
+        bits = sign | 0x7F800000u | (man << 13) | (man ? 0x00400000u : 0u);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// fp32 → fp16 → fp32 with round-to-nearest-even (the Half cast of IntegerDot.cs:82).
+__device__ inline float round_to_half(float f)
+{
+    return (float)(_Float16)f;
+}
+
+template <int TYPE> struct BlockFmt;
+template <> struct BlockFmt<SHS_TYPE_Q4_0> { static constexpr int TS = 18, QS = 2, QH = -1, M = -1; };
+template <> struct BlockFmt<SHS_TYPE_Q4_1> { static constexpr int TS = 20, QS = 4, QH = -1, M = 2; };
+template <> struct BlockFmt<SHS_TYPE_Q5_0> { static constexpr int TS = 22, QS = 6, QH = 2, M = -1; };
+template <> struct BlockFmt<SHS_TYPE_Q5_1> { static constexpr int TS = 24, QS = 8, QH = 4, M = 2; };
+template <> struct BlockFmt<SHS_TYPE_Q8_0> { static constexpr int TS = 34, QS = 2, QH = -1, M = -1; };
+
+// Position p of a stored 32-byte block → quant element index: [0..7, 16..23, 8..15, 24..31].
+__host__ __device__ inline int perm_elem(int p) { return p < 8 ? p : p < 16 ? p + 8 : p < 24 ? p - 8 : p; }
+
+// ------------------------------------------------------------------ repack
+
+template <int TYPE>
+__global__ void k_repack(const uint8_t* __restrict__ native, int row0, int nrows, int B,
+                         uint8_t* __restrict__ qs, uint32_t* __restrict__ qh, float* __restrict__ d,
+                         float* __restrict__ m)
+{
+    typedef BlockFmt<TYPE> F;
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)nrows * B) return;
+    int rr = (int)(idx / B), b = (int)(idx % B);
+    int r = row0 + rr;
+    const uint8_t* blk = native + idx * F::TS;
+    int64_t rec = (int64_t)(r >> 5) * B + b;
+    int ri = r & 31;
+    d[rec * 32 + ri] = half_bits_to_float(blk[0] | (blk[1] << 8));
+    if (F::M >= 0) m[rec * 32 + ri] = half_bits_to_float(blk[F::M] | (blk[F::M + 1] << 8));
+    if (F::QH >= 0)
+        qh[rec * 32 + ri] = (uint32_t)blk[F::QH] | ((uint32_t)blk[F::QH + 1] << 8) |
+                            ((uint32_t)blk[F::QH + 2] << 16) | ((uint32_t)blk[F::QH + 3] << 24);
+    if (TYPE == SHS_TYPE_Q8_0) {
+        uint8_t* dst = qs + rec * 1024 + ri * 32;
+        for (int p = 0; p < 32; p++) dst[p] = blk[F::QS + perm_elem(p)];
+    } else {
+        uint8_t* dst = qs + rec * 512 + ri * 16;
+        for (int p = 0; p < 16; p++) dst[p] = blk[F::QS + p];
+    }
+}
+
+hipError_t launch_repack(const DevMatrix& w, const uint8_t* native, int row0, int nrows, hipStream_t s)
+{
+    int64_t n = (int64_t)nrows * w.blocks;
+    dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: hipLaunchKernelGGL(k_repack<SHS_TYPE_Q4_0>, grid, block, 0, s, native, row0, nrows, w.blocks, w.qs, w.qh, w.d, w.m); break;
+    case SHS_TYPE_Q4_1: hipLaunchKernelGGL(k_repack<SHS_TYPE_Q4_1>, grid, block, 0, s, native, row0, nrows, w.blocks, w.qs, w.qh, w.d, w.m); break;
+    case SHS_TYPE_Q5_0: hipLaunchKernelGGL(k_repack<SHS_TYPE_Q5_0>, grid, block, 0, s, native, row0, nrows, w.blocks, w.qs, w.qh, w.d, w.m); break;
+    case SHS_TYPE_Q5_1: hipLaunchKernelGGL(k_repack<SHS_TYPE_Q5_1>, grid, block, 0, s, native, row0, nrows, w.blocks, w.qs, w.qh, w.d, w.m); break;
+    case SHS_TYPE_Q8_0: hipLaunchKernelGGL(k_repack<SHS_TYPE_Q8_0>, grid, block, 0, s, native, row0, nrows, w.blocks, w.qs, w.qh, w.d, w.m); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------- activation quantization
+
+// One 32-value block: IntegerGemm.QuantizeActivations (semantics 0) or
+// IntegerDot.QuantizeActivations (semantics 1). d = max/127 and 1/d are IEEE
+// (correctly rounded division is on for this file).
+__device__ inline void quant32(const float* v, int semantics, int8_t* q, float& dd, float& ds)
+{
+    float mx = 0.0f;
+    for (int k = 0; k < 32; k++) mx = fmaxf(mx, fabsf(v[k]));
+    float d = mx / 127.0f;
+    float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    int sum = 0;
+    if (semantics == 0) {
+        for (int k = 0; k < 32; k++) {
+            int qi = (int)__builtin_rintf(v[k] * inv);
+            q[k] = (int8_t)qi;
+            sum += qi;
+        }
+        dd = d;
+    } else {
+        for (int k = 0; k < 32; k++) {
+            int qi = (int)roundf(v[k] * inv);
+            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
+            q[k] = (int8_t)qi;
+            sum += qi;
+        }
+        dd = round_to_half(d);
+    }
+    ds = dd * (float)sum;
+}
+
+__device__ inline void store_q8_block(const ActQ8& a, int t, int b, const int8_t* q, float dd, float ds)
+{
+    uint32_t w[8];
+    for (int p4 = 0; p4 < 8; p4++) {
+        uint32_t x = 0;
+        for (int k = 0; k < 4; k++) x |= (uint32_t)(uint8_t)q[perm_elem(4 * p4 + k)] << (8 * k);
+        w[p4] = x;
+    }
+    int8_t* dst = a.q + ((int64_t)(t >> 5) * a.B + b) * 1024 + (t & 31) * 32;
+    reinterpret_cast<uint4*>(dst)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4*>(dst)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    a.d[(int64_t)b * a.Tpad + t] = dd;
+    a.ds[(int64_t)b * a.Tpad + t] = ds;
+}
+
+__device__ inline void store_zero_block(const ActQ8& a, int t, int b)
+{
+    int8_t* dst = a.q + ((int64_t)(t >> 5) * a.B + b) * 1024 + (t & 31) * 32;
+    reinterpret_cast<uint4*>(dst)[0] = make_uint4(0, 0, 0, 0);
+    reinterpret_cast<uint4*>(dst)[1] = make_uint4(0, 0, 0, 0);
+    a.d[(int64_t)b * a.Tpad + t] = 0.0f;
+    a.ds[(int64_t)b * a.Tpad + t] = 0.0f;
+}
+
+__global__ void k_quant_act(const float* __restrict__ x, int ldx, ActQ8 a, int semantics)
+{
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)a.Tpad * a.B) return;
+    int t = (int)(idx % a.Tpad), b = (int)(idx / a.Tpad);
+    if (t >= a.T) { store_zero_block(a, t, b); return; }
+    float v[32];
+    const float4* src = reinterpret_cast<const float4*>(x + (int64_t)t * ldx + 32 * b);
+    for (int k = 0; k < 8; k++) {
+        float4 f = src[k];
+        v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    }
+    int8_t q[32];
+    float dd, ds;
+    quant32(v, semantics, q, dd, ds);
+    store_q8_block(a, t, b, q, dd, ds);
+}
+
+hipError_t launch_quant_act(const float* x, int ldx, const ActQ8& a, int semantics, hipStream_t s)
+{
+    int64_t n = (int64_t)a.Tpad * a.B;
+    hipLaunchKernelGGL(k_quant_act, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, ldx, a, semantics);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------- RMSNorm + quantize
+
+__device__ inline float vsum8(const float* a)
+{
+    return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+}
+
+// Kernels.RmsNorm (Kernels.cs:26-61) in its own order — 16 running float sums of x²
+// (8 "even" lanes, 8 "odd" lanes of Vector<float>), each pairwise-summed and widened to
+// double — followed by y = (x·s)·w and the 32-block quantization of y. One block per token.
+__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x, int ldx,
+                                                       const float* __restrict__ w, float eps, int n,
+                                                       ActQ8 a, float* __restrict__ y_opt)
+{
+    extern __shared__ float sx[];
+    __shared__ float part[16];
+    __shared__ float s_scale;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (t >= a.T) {
+        for (int b = tid; b < a.B; b += blockDim.x) store_zero_block(a, t, b);
+        return;
+    }
+    const float* xr = x + (int64_t)t * ldx;
+    for (int i = tid; i < n; i += blockDim.x) sx[i] = xr[i];
+    __syncthreads();
+    if (tid < 16) {
+        float acc = 0.0f;
+        for (int i = 0; i + 16 <= n; i += 16) {
+            float v = sx[i + tid];
+            acc = acc + v * v;
+        }
+        part[tid] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        double sum = 0.0;
+        int i = 0;
+        if (n >= 16) {
+            sum = (double)vsum8(part) + (double)vsum8(part + 8);
+            i = n / 16 * 16;
+        }
+        for (; i < n; i++) sum += (double)sx[i] * (double)sx[i];
+        s_scale = 1.0f / sqrtf((float)(sum / n) + eps);
+    }
+    __syncthreads();
+    const float sc = s_scale;
+    for (int b = tid; b < a.B; b += blockDim.x) {
+        float v[32];
+        for (int k = 0; k < 32; k++) {
+            float p = sx[32 * b + k] * sc;
+            v[k] = p * w[32 * b + k];
+        }
+        if (y_opt) {
+            float* yr = y_opt + (int64_t)t * n + 32 * b;
+            for (int k = 0; k < 32; k++) yr[k] = v[k];
+        }
+        int8_t q[32];
+        float dd, ds;
+        quant32(v, 0, q, dd, ds);
+        store_q8_block(a, t, b, q, dd, ds);
+    }
+}
+
+hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float eps, int n, const ActQ8& a,
+                                float* y_opt, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(a.Tpad), dim3(256), sizeof(float) * n, s, x, ldx, w, eps, n, a, y_opt);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------- SwiGLU + quantize
+
+// Kernels.SwiGlu (Kernels.cs:83-90): gu = g·u, s = 1/(1+e^−g), y = s·gu; then the
+// 32-block quantization of y for the down projection. gu rows hold [gate | up].
+__global__ void k_swiglu_quant(const float* __restrict__ gu, int ldgu, int ffn, ActQ8 a, float* __restrict__ y_opt)
+{
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)a.Tpad * a.B) return;
+    int t = (int)(idx % a.Tpad), b = (int)(idx / a.Tpad);
+    if (t >= a.T) { store_zero_block(a, t, b); return; }
+    const float* g = gu + (int64_t)t * ldgu + 32 * b;
+    const float* u = g + ffn;
+    float v[32];
+    for (int k = 0; k < 32; k++) {
+        float gv = g[k];
+        float prod = gv * u[k];
+        float sg = 1.0f / (1.0f + expf(-gv));
+        v[k] = sg * prod;
+    }
+    if (y_opt) {
+        float* yr = y_opt + (int64_t)t * ffn + 32 * b;
+        for (int k = 0; k < 32; k++) yr[k] = v[k];
+    }
+    int8_t q[32];
+    float dd, ds;
+    quant32(v, 0, q, dd, ds);
+    store_q8_block(a, t, b, q, dd, ds);
+}
+
+hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& a, float* y_opt, hipStream_t s)
+{
+    int64_t n = (int64_t)a.Tpad * a.B;
+    hipLaunchKernelGGL(k_swiglu_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gu, ldgu, ffn, a, y_opt);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------- GEMM
+
+// Four 4-bit fifth-bit flags → 0x10 in the byte of each set bit.
+__device__ inline uint32_t expand_bits4(uint32_t x4)
+{
+    return ((__umul24(x4, 0x00204081u)) & 0x01010101u) << 4;
+}
+
+// The 16 signed weights lane half h feeds the MFMA, from the row's 16 qs bytes (dwords
+// q0 = bytes 8h..8h+3, q1 = 8h+4..8h+7) and the fifth bits: register bytes are quant
+// elements [8h..8h+7, 16+8h..16+8h+7], i.e. w = u − z with z = 8 (Q4_0), 16 (Q5_0) or 0.
+template <int TYPE>
+__device__ inline v4i unpack_half(uint32_t q0, uint32_t q1, uint32_t qh, int h)
+{
+    uint32_t lo0 = q0 & 0x0F0F0F0Fu, lo1 = q1 & 0x0F0F0F0Fu;
+    uint32_t hi0 = (q0 >> 4) & 0x0F0F0F0Fu, hi1 = (q1 >> 4) & 0x0F0F0F0Fu;
+    if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) {
+        uint32_t sh = 8u * h;
+        lo0 |= expand_bits4((qh >> sh) & 0xFu);
+        lo1 |= expand_bits4((qh >> (sh + 4)) & 0xFu);
+        hi0 |= expand_bits4((qh >> (sh + 16)) & 0xFu);
+        hi1 |= expand_bits4((qh >> (sh + 20)) & 0xFu);
+    }
+    if (TYPE == SHS_TYPE_Q4_0) {
+        lo0 = (lo0 + 0x78787878u) ^ 0x80808080u; lo1 = (lo1 + 0x78787878u) ^ 0x80808080u;
+        hi0 = (hi0 + 0x78787878u) ^ 0x80808080u; hi1 = (hi1 + 0x78787878u) ^ 0x80808080u;
+    } else if (TYPE == SHS_TYPE_Q5_0) {
+        lo0 = (lo0 + 0x70707070u) ^ 0x80808080u; lo1 = (lo1 + 0x70707070u) ^ 0x80808080u;
+        hi0 = (hi0 + 0x70707070u) ^ 0x80808080u; hi1 = (hi1 + 0x70707070u) ^ 0x80808080u;
+    }
+    v4i r;
+    r[0] = (int)lo0; r[1] = (int)lo1; r[2] = (int)hi0; r[3] = (int)hi1;
+    return r;
+}
+
+template <int TYPE>
+__device__ inline v4i load_weights(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh, int64_t rec,
+                                   int ri, int h)
+{
+    if (TYPE == SHS_TYPE_Q8_0) {
+        return *reinterpret_cast<const v4i*>(wqs + rec * 1024 + ri * 32 + h * 16);
+    } else {
+        uint2 q = *reinterpret_cast<const uint2*>(wqs + rec * 512 + ri * 16 + h * 8);
+        uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
+        return unpack_half<TYPE>(q.x, q.y, qh, h);
+    }
+}
+
+// One wave: a 32-row tile × TT 32-token tiles, K consumed one 32-wide quant block per
+// v_mfma_i32_32x32x32_i8. D[i][j] (row i, token j) sits in lane j + 32·(i%8 / 4), register
+// 4·(i/8) + i%4. Each output then takes, block by block in order, exactly the reference's
+// acc = fma(float(I), RN(d_w·d_a), acc) (+ fma(m_w, RN(d_a·Σq), acc) for offset types).
+template <int TYPE, int TT, int MODE>
+__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                                              const float* __restrict__ wd, const float* __restrict__ wm,
+                                              int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N)
+{
+    constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 31, h = lane >> 5;
+    const int rt = blockIdx.x * 4 + wave;
+    if (rt >= ntiles) return;
+    const int ntt = a.Tpad >> 5;
+    const int tt0 = blockIdx.y * TT;
+    int nv = ntt - tt0;
+    nv = nv < TT ? nv : TT;
+
+    v16f acc[TT];
+    for (int u = 0; u < TT; u++)
+        for (int r = 0; r < 16; r++) acc[u][r] = 0.0f;
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+    for (int b = 0; b < B; ++b) {
+        const int64_t rec = (int64_t)rt * B + b;
+        const v4i wv = load_weights<TYPE>(wqs, wqh, rec, j, h);
+        float dw[16], mw[16];
+        const float4* dp = reinterpret_cast<const float4*>(wd + rec * 32);
+        for (int g = 0; g < 4; g++) {
+            float4 v = dp[2 * g + h];
+            dw[4 * g] = v.x; dw[4 * g + 1] = v.y; dw[4 * g + 2] = v.z; dw[4 * g + 3] = v.w;
+        }
+        if (OFF) {
+            const float4* mp = reinterpret_cast<const float4*>(wm + rec * 32);
+            for (int g = 0; g < 4; g++) {
+                float4 v = mp[2 * g + h];
+                mw[4 * g] = v.x; mw[4 * g + 1] = v.y; mw[4 * g + 2] = v.z; mw[4 * g + 3] = v.w;
+            }
+        }
+        for (int u = 0; u < TT; u++) {
+            if (u >= nv) break;
+            const int tile = tt0 + u;
+            const v4i xv = *reinterpret_cast<const v4i*>(a.q + ((int64_t)tile * B + b) * 1024 + j * 32 + h * 16);
+            const float da = a.d[(int64_t)b * a.Tpad + tile * 32 + j];
+            const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(wv, xv, zero, 0, 0, 0);
+            for (int r = 0; r < 16; r++) {
+                float sc = dw[r] * da;
+                acc[u][r] = fmaf((float)D[r], sc, acc[u][r]);
+            }
+            if (OFF) {
+                const float dsv = a.ds[(int64_t)b * a.Tpad + tile * 32 + j];
+                for (int r = 0; r < 16; r++) acc[u][r] = fmaf(mw[r], dsv, acc[u][r]);
+            }
+        }
+    }
+
+    const bool vec = ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
+    for (int u = 0; u < TT; u++) {
+        if (u >= nv) break;
+        const int token = (tt0 + u) * 32 + j;
+        if (token >= a.T) continue;
+        float* yr = y + (int64_t)token * ldy;
+        for (int g = 0; g < 4; g++) {
+            const int row = rt * 32 + 8 * g + 4 * h;
+            if (vec && row + 3 < N) {
+                float4* p = reinterpret_cast<float4*>(yr + row);
+                float4 v = make_float4(acc[u][4 * g], acc[u][4 * g + 1], acc[u][4 * g + 2], acc[u][4 * g + 3]);
+                if (MODE == GEMM_ADD) {
+                    float4 o = *p;
+                    v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+                }
+                *p = v;
+            } else {
+                for (int k = 0; k < 4; k++) {
+                    if (row + k >= N) break;
+                    float v = acc[u][4 * g + k];
+                    if (MODE == GEMM_ADD) v = yr[row + k] + v;
+                    yr[row + k] = v;
+                }
+            }
+        }
+    }
+}
+
+template <int TYPE, int TT>
+static hipError_t gemm_tt(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+{
+    dim3 grid((unsigned)((w.tiles + 3) / 4), (unsigned)(((a.Tpad >> 5) + TT - 1) / TT)), block(256);
+    if (mode == GEMM_ADD)
+        hipLaunchKernelGGL((k_gemm<TYPE, TT, GEMM_ADD>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy, w.rows);
+    else
+        hipLaunchKernelGGL((k_gemm<TYPE, TT, GEMM_STORE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy, w.rows);
+    return hipGetLastError();
+}
+
+template <int TYPE>
+static hipError_t gemm_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+{
+    int ntt = a.Tpad >> 5;
+    if (ntt <= 1) return gemm_tt<TYPE, 1>(w, a, y, ldy, mode, s);
+    if (ntt <= 2) return gemm_tt<TYPE, 2>(w, a, y, ldy, mode, s);
+    return gemm_tt<TYPE, 4>(w, a, y, ldy, mode, s);
+}
+
+hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+{
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: return gemm_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q4_1: return gemm_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q5_0: return gemm_type<SHS_TYPE_Q5_0>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q5_1: return gemm_type<SHS_TYPE_Q5_1>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q8_0: return gemm_type<SHS_TYPE_Q8_0>(w, a, y, ldy, mode, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// The raw MFMA int32 block sums, out[t][r][b] — parity instrumentation.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_gemm_sums(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                                                   int ntiles, int B, ActQ8 a, int32_t* __restrict__ out, int N)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 31, h = lane >> 5;
+    const int rt = blockIdx.x * 4 + wave;
+    if (rt >= ntiles) return;
+    const int tile = blockIdx.y;
+    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const int token = tile * 32 + j;
+    for (int b = 0; b < B; ++b) {
+        const int64_t rec = (int64_t)rt * B + b;
+        const v4i wv = load_weights<TYPE>(wqs, wqh, rec, j, h);
+        const v4i xv = *reinterpret_cast<const v4i*>(a.q + ((int64_t)tile * B + b) * 1024 + j * 32 + h * 16);
+        const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(wv, xv, zero, 0, 0, 0);
+        if (token < a.T)
+            for (int r = 0; r < 16; r++) {
+                const int row = rt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < N) out[((int64_t)token * N + row) * B + b] = D[r];
+            }
+    }
+}
+
+hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* out, hipStream_t s)
+{
+    dim3 grid((unsigned)((w.tiles + 3) / 4), (unsigned)(a.Tpad >> 5)), block(256);
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: hipLaunchKernelGGL(k_gemm_sums<SHS_TYPE_Q4_0>, grid, block, 0, s, w.qs, w.qh, w.tiles, w.blocks, a, out, w.rows); break;
+    case SHS_TYPE_Q4_1: hipLaunchKernelGGL(k_gemm_sums<SHS_TYPE_Q4_1>, grid, block, 0, s, w.qs, w.qh, w.tiles, w.blocks, a, out, w.rows); break;
+    case SHS_TYPE_Q5_0: hipLaunchKernelGGL(k_gemm_sums<SHS_TYPE_Q5_0>, grid, block, 0, s, w.qs, w.qh, w.tiles, w.blocks, a, out, w.rows); break;
+    case SHS_TYPE_Q5_1: hipLaunchKernelGGL(k_gemm_sums<SHS_TYPE_Q5_1>, grid, block, 0, s, w.qs, w.qh, w.tiles, w.blocks, a, out, w.rows); break;
+    case SHS_TYPE_Q8_0: hipLaunchKernelGGL(k_gemm_sums<SHS_TYPE_Q8_0>, grid, block, 0, s, w.qs, w.qh, w.tiles, w.blocks, a, out, w.rows); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------ GEMV (selected rows)
+
+// One thread per (token, selected row): the same exact integer block sums (v_dot4_i32_i8
+// on the same byte pairing the MFMA lanes use) and the same serial epilogue, so every
+// value equals the corresponding entry of the full GEMM bit for bit
+// (QuantMatMul.ForwardRowsAsync, QuantMatMul.cs:98-110).
+template <int TYPE>
+__global__ void k_gemv_rows(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                            const float* __restrict__ wd, const float* __restrict__ wm, int B,
+                            const int32_t* __restrict__ ids, int n_ids, ActQ8 a, float* __restrict__ y)
+{
+    constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)a.T * n_ids) return;
+    const int i = (int)(idx % n_ids), t = (int)(idx / n_ids);
+    const int r = ids[i];
+    const int ri = r & 31;
+    float acc = 0.0f;
+    for (int b = 0; b < B; ++b) {
+        const int64_t rec = (int64_t)(r >> 5) * B + b;
+        const uint4* ap = reinterpret_cast<const uint4*>(a.q + ((int64_t)(t >> 5) * B + b) * 1024 + (t & 31) * 32);
+        const uint4 a0 = ap[0], a1 = ap[1];
+        v4i w0, w1;
+        if (TYPE == SHS_TYPE_Q8_0) {
+            const v4i* wp = reinterpret_cast<const v4i*>(wqs + rec * 1024 + ri * 32);
+            w0 = wp[0];
+            w1 = wp[1];
+        } else {
+            const uint4 q = *reinterpret_cast<const uint4*>(wqs + rec * 512 + ri * 16);
+            const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
+            w0 = unpack_half<TYPE>(q.x, q.y, qh, 0);
+            w1 = unpack_half<TYPE>(q.z, q.w, qh, 1);
+        }
+        int I = 0;
+        I = __builtin_amdgcn_sdot4(w0[0], (int)a0.x, I, false);
+        I = __builtin_amdgcn_sdot4(w0[1], (int)a0.y, I, false);
+        I = __builtin_amdgcn_sdot4(w0[2], (int)a0.z, I, false);
+        I = __builtin_amdgcn_sdot4(w0[3], (int)a0.w, I, false);
+        I = __builtin_amdgcn_sdot4(w1[0], (int)a1.x, I, false);
+        I = __builtin_amdgcn_sdot4(w1[1], (int)a1.y, I, false);
+        I = __builtin_amdgcn_sdot4(w1[2], (int)a1.z, I, false);
+        I = __builtin_amdgcn_sdot4(w1[3], (int)a1.w, I, false);
+        const float da = a.d[(int64_t)b * a.Tpad + t];
+        const float sc = wd[rec * 32 + ri] * da;
+        acc = fmaf((float)I, sc, acc);
+        if (OFF) acc = fmaf(wm[rec * 32 + ri], a.ds[(int64_t)b * a.Tpad + t], acc);
+    }
+    y[(int64_t)t * n_ids + i] = acc;
+}
+
+hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* ids, int n_ids, float* y,
+                            hipStream_t s)
+{
+    int64_t n = (int64_t)a.T * n_ids;
+    dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q4_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q4_1: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q4_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q5_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q5_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q5_1: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q5_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q8_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q8_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// -------------------------------------------------------- embedding gather
+
+// QuantMatMul.GatherRows → Dequantizer (QuantMatMul.cs:534-545, Dequantizer.cs:127-213),
+// read from the repacked table: one thread per (token, block).
+template <int TYPE>
+__global__ void k_embed(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh, const float* __restrict__ wd,
+                        const float* __restrict__ wm, int B, const int32_t* __restrict__ ids, int n,
+                        float* __restrict__ h, int ldh)
+{
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)n * B) return;
+    const int b = (int)(idx % B), t = (int)(idx / B);
+    const int r = ids[t], ri = r & 31;
+    const int64_t rec = (int64_t)(r >> 5) * B + b;
+    const float d = wd[rec * 32 + ri];
+    float* out = h + (int64_t)t * ldh + 32 * b;
+    if (TYPE == SHS_TYPE_Q8_0) {
+        const int8_t* q = reinterpret_cast<const int8_t*>(wqs + rec * 1024 + ri * 32);
+        for (int p = 0; p < 32; p++) out[perm_elem(p)] = (float)q[p] * d;
+        return;
+    }
+    const uint8_t* q = wqs + rec * 512 + ri * 16;
+    const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
+    const float m = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1) ? wm[rec * 32 + ri] : 0.0f;
+    for (int jj = 0; jj < 16; jj++) {
+        int lo = q[jj] & 0x0F, hi = q[jj] >> 4;
+        if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) {
+            lo |= (int)(((qh >> jj) & 1u) << 4);
+            hi |= (int)(((qh >> (jj + 16)) & 1u) << 4);
+        }
+        if (TYPE == SHS_TYPE_Q4_0) { out[jj] = d * (float)(lo - 8); out[16 + jj] = d * (float)(hi - 8); }
+        else if (TYPE == SHS_TYPE_Q5_0) { out[jj] = d * (float)(lo - 16); out[16 + jj] = d * (float)(hi - 16); }
+        else { float a0 = d * (float)lo; float a1 = d * (float)hi; out[jj] = a0 + m; out[16 + jj] = a1 + m; }
+    }
+}
+
+hipError_t launch_embed(const DevMatrix& w, const int32_t* ids, int n, float* h, int ldh, hipStream_t s)
+{
+    int64_t cnt = (int64_t)n * w.blocks;
+    dim3 grid((unsigned)((cnt + 255) / 256)), block(256);
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: hipLaunchKernelGGL(k_embed<SHS_TYPE_Q4_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n, h, ldh); break;
+    case SHS_TYPE_Q4_1: hipLaunchKernelGGL(k_embed<SHS_TYPE_Q4_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n, h, ldh); break;
+    case SHS_TYPE_Q5_0: hipLaunchKernelGGL(k_embed<SHS_TYPE_Q5_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n, h, ldh); break;
+    case SHS_TYPE_Q5_1: hipLaunchKernelGGL(k_embed<SHS_TYPE_Q5_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n, h, ldh); break;
+    case SHS_TYPE_Q8_0: hipLaunchKernelGGL(k_embed<SHS_TYPE_Q8_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n, h, ldh); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------ RoPE + KV store
+
+// Rope.Apply on adjacent pairs (Rope.cs:112-135) with host-computed cos/sin tables,
+// ApplyPositionScale on queries (MinistralModel.cs:476-482), and StoreKeys/StoreValues
+// (MinistralModel.cs:452-469). One wave per (token, head) of [q heads | k heads | v heads].
+__global__ __launch_bounds__(64) void k_rope_store(float* __restrict__ qkv, int ld, int n_head, int n_kv, int hd,
+                                                   const int32_t* __restrict__ pos, const float* __restrict__ ct,
+                                                   const float* __restrict__ st, const float* __restrict__ qscale,
+                                                   int half, float* __restrict__ kc, float* __restrict__ vc, int cap,
+                                                   int slot0)
+{
+    const int t = blockIdx.x, hh = blockIdx.y, tid = threadIdx.x;
+    const int p = pos[t];
+    float* row = qkv + (int64_t)t * ld;
+    if (hh < n_head + n_kv) {
+        float* x = row + (int64_t)hh * hd;
+        const float* c = ct + (int64_t)p * half;
+        const float* s = st + (int64_t)p * half;
+        for (int i = tid; i < half; i += 64) {
+            float x0 = x[2 * i], x1 = x[2 * i + 1];
+            float a = x0 * c[i], bb = x1 * s[i];
+            float e = x0 * s[i], f = x1 * c[i];
+            x[2 * i] = a - bb;
+            x[2 * i + 1] = e + f;
+        }
+        if (hh < n_head) {
+            const float qs = qscale[p];
+            if (qs != 1.0f) {
+                __syncthreads();
+                for (int i = tid; i < hd; i += 64) x[i] = x[i] * qs;
+            }
+        } else {
+            __syncthreads();
+            const int kh = hh - n_head;
+            float* dst = kc + ((int64_t)kh * cap + slot0 + t) * hd;
+            for (int i = tid; i < hd; i += 64) dst[i] = x[i];
+        }
+    } else {
+        const int kh = hh - n_head - n_kv;
+        const float* x = row + (int64_t)(n_head + n_kv + kh) * hd;
+        float* dst = vc + ((int64_t)kh * cap + slot0 + t) * hd;
+        for (int i = tid; i < hd; i += 64) dst[i] = x[i];
+    }
+}
+
+hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv, int hd, const int32_t* pos,
+                             const float* ct, const float* st, const float* qscale, int half, float* kc, float* vc,
+                             int cap, int slot0, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_rope_store, dim3(T, n_head + 2 * n_kv), dim3(64), 0, s, qkv, ldqkv, n_head, n_kv, hd, pos, ct, st,
+                       qscale, half, kc, vc, cap, slot0);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ attention
+
+// Causal GQA attention (MinistralModel.AttendGroup, MinistralModel.cs:372-440) as an
+// online-softmax pass over 32-key tiles. A block holds the 4 query heads of one KV head
+// for ≤32 queries; K (transposed) and V tiles are staged in LDS once for all four.
+// Scores S^T = K·Q^T and context O^T = V^T·P^T run on v_mfma_f32_32x32x2f32 (fp32
+// products, fp32 accumulation): lane j (query) holds 16 keys / 16 dims per tile.
+constexpr int ATT_HD = 128;
+
+__global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
+                                                   const float* __restrict__ vc, int cap,
+                                                   const AttnItem* __restrict__ items, int n_items, int n_head,
+                                                   int n_kv, float scale, float* __restrict__ ctx, int ldc)
+{
+    __shared__ float Ks[ATT_HD * 32];
+    __shared__ float Vs[32 * ATT_HD];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 31, h = lane >> 5;
+    const AttnItem it = items[n_items - 1 - blockIdx.x];
+    const int kvh = blockIdx.y;
+    const int group = n_head / n_kv;
+    const int head = kvh * group + wave;
+    const float* kb = kc + (int64_t)kvh * cap * ATT_HD;
+    const float* vb = vc + (int64_t)kvh * cap * ATT_HD;
+
+    const bool qvalid = j < it.q_count;
+    float qr[64];
+    {
+        const float* qrow = q + (int64_t)(it.q_start + (qvalid ? j : 0)) * ldq + head * ATT_HD + 64 * h;
+        for (int c = 0; c < 64; c += 4) {
+            float4 v = qvalid ? *reinterpret_cast<const float4*>(qrow + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            qr[c] = v.x; qr[c + 1] = v.y; qr[c + 2] = v.z; qr[c + 3] = v.w;
+        }
+    }
+    float m_run = -INFINITY, l_run = 0.0f;
+    v16f o[4];
+    for (int dt = 0; dt < 4; dt++)
+        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+
+    const int n_keys = it.pos0 + it.q_count;
+    const int qpos = it.pos0 + j;
+    const int n_kt = (n_keys + 31) >> 5;
+    for (int kt = 0; kt < n_kt; ++kt) {
+        __syncthreads();
+        for (int e = threadIdx.x; e < 32 * 32; e += blockDim.x) {
+            const int key = e & 31, d4 = e >> 5;
+            const int kidx = kt * 32 + key;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (kidx < n_keys) {
+                const int64_t off = (int64_t)(it.key_start + kidx) * ATT_HD + 4 * d4;
+                kv = *reinterpret_cast<const float4*>(kb + off);
+                vv = *reinterpret_cast<const float4*>(vb + off);
+            }
+            Ks[(4 * d4 + 0) * 32 + key] = kv.x;
+            Ks[(4 * d4 + 1) * 32 + key] = kv.y;
+            Ks[(4 * d4 + 2) * 32 + key] = kv.z;
+            Ks[(4 * d4 + 3) * 32 + key] = kv.w;
+            *reinterpret_cast<float4*>(&Vs[key * ATT_HD + 4 * d4]) = vv;
+        }
+        __syncthreads();
+        if (group <= wave) continue;
+
+        v16f s;
+        for (int r = 0; r < 16; r++) s[r] = 0.0f;
+        for (int c = 0; c < 64; ++c)
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(64 * h + c) * 32 + j], qr[c], s, 0, 0, 0);
+
+        float p[16];
+        float tmax = -INFINITY;
+        for (int r = 0; r < 16; r++) {
+            const int key = kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            float sv = s[r] * scale;
+            if (key > qpos || !qvalid) sv = -INFINITY;
+            p[r] = sv;
+            tmax = fmaxf(tmax, sv);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run, tmax);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = expf(m_run - m_use);
+        float rs = 0.0f;
+        for (int r = 0; r < 16; r++) {
+            p[r] = expf(p[r] - m_use);
+            rs += p[r];
+        }
+        rs += __shfl_xor(rs, 32);
+        l_run = l_run * alpha + rs;
+        m_run = m_new;
+        for (int dt = 0; dt < 4; dt++)
+            for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
+        for (int dt = 0; dt < 4; dt++)
+            for (int c = 0; c < 16; c++) {
+                const int key = 8 * (c >> 2) + 4 * h + (c & 3);
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * ATT_HD + 32 * dt + j], p[c], o[dt], 0, 0, 0);
+            }
+    }
+    if (!qvalid || wave >= group) return;
+    float* out = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD;
+    for (int dt = 0; dt < 4; dt++)
+        for (int g = 0; g < 4; g++) {
+            const int dim = 32 * dt + 8 * g + 4 * h;
+            float4 v = make_float4(o[dt][4 * g] / l_run, o[dt][4 * g + 1] / l_run, o[dt][4 * g + 2] / l_run,
+                                   o[dt][4 * g + 3] / l_run);
+            *reinterpret_cast<float4*>(out + dim) = v;
+        }
+}
+
+hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
+                            int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
+                            hipStream_t s)
+{
+    if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attention, dim3(n_items, n_kv), dim3(256), 0, s, q, ldq, kc, vc, cap, items, n_items, n_head,
+                       n_kv, scale, ctx, ldc);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ utilities
+
+__global__ void k_copy_rows(const float* __restrict__ src, int lds, float* __restrict__ dst, int ldd, int rows, int cols)
+{
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)rows * cols) return;
+    int r = (int)(idx / cols), c = (int)(idx % cols);
+    dst[(int64_t)r * ldd + c] = src[(int64_t)r * lds + c];
+}
+
+hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s)
+{
+    int64_t n = (int64_t)rows * cols;
+    hipLaunchKernelGGL(k_copy_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, lds, dst, ldd, rows, cols);
+    return hipGetLastError();
+}
+
+__global__ void k_fill_zero(float* p, size_t n)
+{
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < n) p[idx] = 0.0f;
+}
+
+hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n);
+    return hipGetLastError();
+}
+
+// Kernels.Add (Kernels.cs:64): a ← a + b.
+__global__ void k_add_inplace(float* __restrict__ a, const float* __restrict__ b, size_t n)
+{
+    size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < n) a[idx] = a[idx] + b[idx];
+}
+
+hipError_t launch_add_inplace(float* a, const float* b, size_t n, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_add_inplace, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, n);
+    return hipGetLastError();
+}
+
+__global__ void k_gather_rows(const float* __restrict__ src, int lds, const int32_t* __restrict__ rows, int n, int cols,
+                              float* __restrict__ dst, int ldd)
+{
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)n * cols) return;
+    int r = (int)(idx / cols), c = (int)(idx % cols);
+    dst[(int64_t)r * ldd + c] = src[(int64_t)rows[r] * lds + c];
+}
+
+hipError_t launch_gather_rows(const float* src, int lds, const int32_t* rows, int n, int cols, float* dst, int ldd,
+                              hipStream_t s)
+{
+    int64_t cnt = (int64_t)n * cols;
+    if (cnt == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_gather_rows, dim3((unsigned)((cnt + 255) / 256)), dim3(256), 0, s, src, lds, rows, n, cols, dst, ldd);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------ synthetic weights
+
+__device__ inline uint64_t mix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Two standard normals (Box–Muller) from counter c of stream (seed, tensor).
+__device__ inline void normal_pair(uint64_t seed, uint64_t tensor, uint64_t c, float* z0, float* z1)
+{
+    uint64_t u = mix64(seed ^ mix64((tensor << 40) ^ c));
+    float u1 = (float)((u >> 40) + 1) * (1.0f / 16777216.0f);
+    float u2 = (float)(u & 0xFFFFFFu) * (1.0f / 16777216.0f);
+    float r = sqrtf(-2.0f * logf(u1));
+    float a = 6.283185307179586f * u2;
+    *z0 = r * cosf(a);
+    *z1 = r * sinf(a);
+}
+
+__device__ inline void wr_half(uint8_t* p, float f)
+{
+    _Float16 h = (_Float16)f;
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    p[0] = (uint8_t)b;
+    p[1] = (uint8_t)(b >> 8);
+}
+
+// ggml block quantizers (gguf-py quants.py rules) for one 32-value block.
+__device__ void quantize_block(int type, const float* x, uint8_t* p)
+{
+    int q[32];
+    if (type == SHS_TYPE_Q4_0 || type == SHS_TYPE_Q5_0) {
+        const bool five = type == SHS_TYPE_Q5_0;
+        float amax = 0.0f, mx = 0.0f;
+        for (int j = 0; j < 32; j++)
+            if (fabsf(x[j]) > amax) { amax = fabsf(x[j]); mx = x[j]; }
+        float d = mx / (five ? -16.0f : -8.0f);
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t qh = 0;
+        for (int j = 0; j < 32; j++) {
+            double t = (double)x[j] * (double)id;
+            t = t + (five ? 16.5 : 8.5);
+            int v = (int)truncf((float)t);
+            v = v < 0 ? 0 : (v > (five ? 31 : 15) ? (five ? 31 : 15) : v);
+            q[j] = v;
+            qh |= (uint32_t)((v >> 4) & 1) << j;
+        }
+        wr_half(p, d);
+        uint8_t* qs = p + 2;
+        if (five) {
+            for (int k = 0; k < 4; k++) p[2 + k] = (uint8_t)(qh >> (8 * k));
+            qs = p + 6;
+        }
+        for (int j = 0; j < 16; j++) qs[j] = (uint8_t)((q[j] & 0x0F) | ((q[16 + j] & 0x0F) << 4));
+    } else if (type == SHS_TYPE_Q4_1 || type == SHS_TYPE_Q5_1) {
+        const bool five = type == SHS_TYPE_Q5_1;
+        float mx = x[0], mn = x[0];
+        for (int j = 1; j < 32; j++) { mx = fmaxf(mx, x[j]); mn = fminf(mn, x[j]); }
+        float d = (mx - mn) / (five ? 31.0f : 15.0f);
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t qh = 0;
+        for (int j = 0; j < 32; j++) {
+            float a = x[j] - mn;
+            a = a * id;
+            a = a + 0.5f;
+            int v = (int)truncf(a);
+            v = v < 0 ? 0 : (v > (five ? 31 : 15) ? (five ? 31 : 15) : v);
+            q[j] = v;
+            qh |= (uint32_t)((v >> 4) & 1) << j;
+        }
+        wr_half(p, d);
+        wr_half(p + 2, mn);
+        uint8_t* qs = p + 4;
+        if (five) {
+            for (int k = 0; k < 4; k++) p[4 + k] = (uint8_t)(qh >> (8 * k));
+            qs = p + 8;
+        }
+        for (int j = 0; j < 16; j++) qs[j] = (uint8_t)((q[j] & 0x0F) | ((q[16 + j] & 0x0F) << 4));
+    } else {  // Q8_0
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
+        float d = amax / 127.0f;
+        float id = d != 0.0f ? 1.0f / d : 0.0f;
+        wr_half(p, d);
+        for (int j = 0; j < 32; j++) {
+            float v = x[j] * id;
+            float a = fabsf(v), fl = floorf(a);
+            float r = fl + floorf(2.0f * (a - fl));
+            p[2 + j] = (uint8_t)(int8_t)(v < 0.0f ? -r : r);
+        }
+    }
+}
+
+__global__ void k_synth_native(int type, int ts, uint64_t seed, uint64_t tensor, int rows, int B, float mean, float std,
+                               uint8_t* __restrict__ native)
+{
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)rows * B) return;
+    float x[32];
+    for (int i = 0; i < 16; i++) {
+        float z0, z1;
+        normal_pair(seed, tensor, (uint64_t)idx * 16 + i, &z0, &z1);
+        x[2 * i] = mean + std * z0;
+        x[2 * i + 1] = mean + std * z1;
+    }
+    quantize_block(type, x, native + idx * ts);
+}
+
+hipError_t launch_synth_native(int type, uint64_t seed, uint64_t tensor, int rows, int cols, float mean, float std,
+                               uint8_t* native, hipStream_t s)
+{
+    int ts = type == SHS_TYPE_Q4_0 ? 18 : type == SHS_TYPE_Q4_1 ? 20 : type == SHS_TYPE_Q5_0 ? 22
+           : type == SHS_TYPE_Q5_1 ? 24 : type == SHS_TYPE_Q8_0 ? 34 : -1;
+    if (ts < 0 || cols % 32) return hipErrorInvalidValue;
+    int B = cols / 32;
+    int64_t n = (int64_t)rows * B;
+    hipLaunchKernelGGL(k_synth_native, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, type, ts, seed, tensor, rows, B,
+                       mean, std, native);
+    return hipGetLastError();
+}
+
+__global__ void k_synth_f32(uint64_t seed, uint64_t tensor, int64_t n, float mean, float std, float* __restrict__ out)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (2 * i >= n) return;
+    float z0, z1;
+    normal_pair(seed, tensor, (uint64_t)i, &z0, &z1);
+    out[2 * i] = mean + std * z0;
+    if (2 * i + 1 < n) out[2 * i + 1] = mean + std * z1;
+}
+
+hipError_t launch_synth_f32(uint64_t seed, uint64_t tensor, int64_t n, float mean, float std, float* out, hipStream_t s)
+{
+    int64_t pairs = (n + 1) / 2;
+    hipLaunchKernelGGL(k_synth_f32, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, seed, tensor, n, mean, std, out);
+    return hipGetLastError();
+}
+
+// -------------------------------------------------------- unpack (inverse)
+
+template <int TYPE>
+__global__ void k_unpack_native(const uint8_t* __restrict__ qs, const uint32_t* __restrict__ qh,
+                                const float* __restrict__ d, const float* __restrict__ m, int row0, int nrows, int B,
+                                uint8_t* __restrict__ native)
+{
+    typedef BlockFmt<TYPE> F;
+    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)nrows * B) return;
+    int rr = (int)(idx / B), b = (int)(idx % B);
+    int r = row0 + rr;
+    uint8_t* blk = native + idx * F::TS;
+    int64_t rec = (int64_t)(r >> 5) * B + b;
+    int ri = r & 31;
+    wr_half(blk, d[rec * 32 + ri]);
+    if (F::M >= 0) wr_half(blk + F::M, m[rec * 32 + ri]);
+    if (F::QH >= 0) {
+        uint32_t v = qh[rec * 32 + ri];
+        for (int k = 0; k < 4; k++) blk[F::QH + k] = (uint8_t)(v >> (8 * k));
+    }
+    if (TYPE == SHS_TYPE_Q8_0) {
+        const uint8_t* src = qs + rec * 1024 + ri * 32;
+        for (int p = 0; p < 32; p++) blk[F::QS + perm_elem(p)] = src[p];
+    } else {
+        const uint8_t* src = qs + rec * 512 + ri * 16;
+        for (int p = 0; p < 16; p++) blk[F::QS + p] = src[p];
+    }
+}
+
+hipError_t launch_unpack_native(const DevMatrix& w, int row0, int nrows, uint8_t* native, hipStream_t s)
+{
+    int64_t n = (int64_t)nrows * w.blocks;
+    dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: hipLaunchKernelGGL(k_unpack_native<SHS_TYPE_Q4_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, row0, nrows, w.blocks, native); break;
+    case SHS_TYPE_Q4_1: hipLaunchKernelGGL(k_unpack_native<SHS_TYPE_Q4_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, row0, nrows, w.blocks, native); break;
+    case SHS_TYPE_Q5_0: hipLaunchKernelGGL(k_unpack_native<SHS_TYPE_Q5_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, row0, nrows, w.blocks, native); break;
+    case SHS_TYPE_Q5_1: hipLaunchKernelGGL(k_unpack_native<SHS_TYPE_Q5_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, row0, nrows, w.blocks, native); break;
+    case SHS_TYPE_Q8_0: hipLaunchKernelGGL(k_unpack_native<SHS_TYPE_Q8_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, row0, nrows, w.blocks, native); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace shs

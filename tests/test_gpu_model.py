@@ -1,0 +1,246 @@
+"""The HIP forward pass (MinistralModel / ShieldstralModerator parity) against the oracle.
+
+Bars: stages that are integer or single IEEE ops (RMSNorm in the reference's order, the
+int8 quantization, the GEMM epilogue, RoPE from the same cos/sin) are compared
+bit-exactly where their inputs are; everything downstream of attention's exp/online
+softmax is held to relative L2 ≤ 1e-4 (the north-star fp32 tolerance), and the Score
+to 1e-4 absolute."""
+import math
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import helpers as H
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layer=2, hidden=256, n_head=4, n_kv_head=1, head_dim=128, ffn=512, vocab=512)
+FP_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def tiny(shs, oracle):
+    cfg = oracle.make_config(**TINY)
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=7)
+    gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=600)
+    return cfg, tensors, types, gpu, ora
+
+
+def test_forward_matches_oracle_and_first_layer_is_bit_exact(shs, oracle, tiny):
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(1).integers(0, cfg.vocab, 77)
+    gcap, ocap = {}, {}
+    gpu.reset_kv_cache()
+    gpu.set_capture(lambda n, a: gcap.__setitem__(n, a))
+    try:
+        g = gpu.forward(toks)
+    finally:
+        gpu.set_capture(None)
+    ora.reset()
+    o = ora.forward(toks, head_mode=2, capture=lambda n, a: ocap.__setitem__(n, a))
+    expected = {"embeddings", "final_norm", "logits"} | {
+        f"blk.{l}.{s}" for l in range(cfg.n_layer) for s in H.CAPTURE_NAMES_PER_LAYER}
+    assert set(gcap) == expected == set(ocap)
+    for name in ("embeddings", "blk.0.attn_norm", "blk.0.q_rope", "blk.0.k_rope", "blk.0.v"):
+        assert np.array_equal(gcap[name], ocap[name]), name
+    for name in expected:
+        assert H.rel_l2(gcap[name], ocap[name]) < FP_TOL, (name, H.rel_l2(gcap[name], ocap[name]))
+    assert H.rel_l2(g, o) < FP_TOL
+
+
+def test_selected_rows_are_bit_identical_to_the_full_head(shs, tiny):
+    """SystemPromptCacheTests.ScoringReadsExactlyWhatTheFullHeadWouldHave."""
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(2).integers(0, cfg.vocab, 40)
+    ids = [3, 400, 3, 511, 0]
+    gpu.reset_kv_cache()
+    full = gpu.forward(toks)
+    gpu.reset_kv_cache()
+    sel = gpu.forward_selected(toks, ids)
+    assert np.array_equal(sel, full[ids])
+
+
+def test_prefix_cache_is_bit_identical(shs, tiny):
+    """SystemPromptCacheTests.CachedAndUncachedProduceIdenticalLogits (all vocab entries)."""
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(3).integers(0, cfg.vocab, 90)
+    gpu.reset_kv_cache()
+    full = gpu.forward(toks)
+    cache = shs.SystemPromptCache.capture(gpu, toks[:37])
+    assert gpu.cached_token_count == 37
+    cache.restore_into(gpu)
+    cached = gpu.forward(toks[37:])
+    assert np.array_equal(full, cached)
+    assert gpu.cached_token_count == 90
+
+
+def test_kv_snapshot_layout_matches_the_oracle(shs, tiny):
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(4).integers(0, cfg.vocab, 45)
+    gpu.reset_kv_cache()
+    gpu.prefill(toks)
+    ora.reset()
+    ora.forward(toks, head_mode=0)
+    snap = gpu.kv_cache.snapshot(45)
+    ref = ora.snapshot(45)
+    assert snap.shape == ref.shape
+    per = cfg.n_kv_head * 45 * cfg.head_dim  # layer 0 keys are bit-exact
+    assert np.array_equal(snap[:per], ref[:per])
+    assert H.rel_l2(snap, ref) < FP_TOL
+    with pytest.raises(shs.ArgumentOutOfRangeError):
+        gpu.kv_cache.snapshot(46)
+    with pytest.raises(shs.ArgumentError):
+        gpu.kv_cache.restore(snap[:-1], 45)
+
+
+def test_kv_cache_grows_without_changing_results(shs, oracle, tiny):
+    cfg, tensors, types, gpu, ora = tiny
+    small = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types, initial_cache_capacity=8)
+    toks = np.random.default_rng(5).integers(0, cfg.vocab, 70)
+    small.prefill(toks[:30])
+    grown = small.forward(toks[30:])
+    assert small.kv_cache.capacity >= 70
+    gpu.reset_kv_cache()
+    assert np.array_equal(grown, gpu.forward(toks))
+    small.close()
+
+
+def test_a_cancelled_pass_leaves_the_instance_usable(shs, tiny):
+    """ModerationCancellationTests: cancellation is observed, the KV length does not move,
+    and the next request scores exactly as a fresh one."""
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(6).integers(0, cfg.vocab, 50)
+    gpu.reset_kv_cache()
+    gpu.prefill(toks[:10])
+    flag = shs.CancellationFlag()
+    flag.cancel()
+    with pytest.raises(shs.OperationCanceledError):
+        gpu.forward_selected(toks[10:], [1, 2], cancel=flag)
+    assert gpu.cached_token_count == 10
+    after = gpu.forward_selected(toks[10:], [1, 2])
+    gpu.reset_kv_cache()
+    assert np.array_equal(after, gpu.forward_selected(toks, [1, 2]))
+
+
+def test_invalid_requests_raise_the_reference_exceptions(shs, tiny):
+    cfg, tensors, types, gpu, ora = tiny
+    gpu.reset_kv_cache()
+    with pytest.raises(shs.ArgumentOutOfRangeError):
+        gpu.forward_selected([1, 2, cfg.vocab], [0])
+    with pytest.raises(shs.ArgumentOutOfRangeError):
+        gpu.forward_selected([1, 2], [cfg.vocab])
+    with pytest.raises(shs.ArgumentError):
+        gpu.forward_selected([], [0])
+    assert gpu.cached_token_count == 0
+
+
+def test_packed_ragged_batch_equals_one_prompt_at_a_time(shs, oracle, tiny):
+    cfg, tensors, types, gpu, ora = tiny
+    rng = np.random.default_rng(7)
+    prompts = [rng.integers(0, cfg.vocab, n) for n in (5, 64, 33, 100, 1)]
+    ids = [7, 8, 9]
+    batch = gpu.forward_batch(prompts, ids)
+    for p, row in zip(prompts, batch):
+        gpu.reset_kv_cache()
+        assert np.array_equal(gpu.forward_selected(p, ids), row)
+        ora.reset()
+        assert H.rel_l2(row, ora.forward(p, head_mode=1, vocab_ids=ids)) < FP_TOL
+
+
+def test_moderator_scores_like_the_oracle(shs, oracle, tiny):
+    cfg, tensors, types, gpu, ora = tiny
+    rng = np.random.default_rng(8)
+    prefix = rng.integers(0, cfg.vocab, 12)
+    yes, no = [10, 11, 12], [20, 21]
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "prefix.shkv")
+        mod = shs.ShieldstralModerator(gpu, yes, no, system_prefix_tokens=prefix, prefix_cache_path=path)
+        assert os.path.exists(path) and mod.cached_prefix_tokens == 12
+        again = shs.SystemPromptCache.try_load(path, gpu)
+        assert again is not None and np.array_equal(again.state, mod._prefix.state)
+        prompt = np.concatenate([prefix, rng.integers(0, cfg.vocab, 40)])
+        r = mod.moderate_tokens(prompt)
+        assert r.prefilled_tokens == 12 and r.prompt_tokens == 52
+        ora.reset()
+        logits = ora.forward(prompt, head_mode=1, vocab_ids=yes + no)
+        s, y, n = oracle.score(logits, 3, 2)
+        assert abs(r.score - s) < 1e-4 and abs(r.yes_logit - y) < 1e-4 * max(1, abs(y))
+        assert r.is_unsafe == (r.score > 0.5) and r.is_unsafe_at(0.0) == (r.score > 0.0)
+        other = rng.integers(0, cfg.vocab, 30)  # no shared prefix: the cache is reset, not restored
+        r2 = mod.moderate_tokens(other)
+        assert r2.prefilled_tokens == 0
+        assert mod.top_verdict_token(prompt) == int(np.argmax(gpu.forward(prompt[12:])))
+
+
+def test_gguf_file_loads_identically_and_bad_files_are_rejected(shs, oracle, tiny):
+    import gguf_writer
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(9).integers(0, cfg.vocab, 30)
+    gpu.reset_kv_cache()
+    ref = gpu.forward(toks)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "tiny.gguf")
+        gguf_writer.write_gguf(path, "mistral3", cfg, tensors, types)
+        m = shs.MinistralModel.open(path)
+        assert m.config.vocab_size == cfg.vocab and m.config.layer_count == cfg.n_layer
+        assert np.array_equal(m.forward(toks), ref)
+        m.close()
+        bad = os.path.join(d, "trunc.gguf")
+        gguf_writer.write_gguf(bad, "mistral3", cfg, tensors, types, truncate_by=100)
+        with pytest.raises(shs.ModelIOError):
+            shs.MinistralModel.open(bad)
+        junk = os.path.join(d, "junk.gguf")
+        with open(junk, "wb") as f:
+            f.write(b"not a gguf at all, just some bytes")
+        with pytest.raises(shs.InvalidDataError):
+            shs.MinistralModel.open(junk)
+        other = os.path.join(d, "other.gguf")
+        gguf_writer.write_gguf(other, "gemma3", cfg, tensors, types)
+        with pytest.raises(shs.NotSupportedError):
+            shs.MinistralModel.open(other)
+        missing = dict(tensors)
+        del missing["blk.1.ffn_up.weight"]
+        gone = os.path.join(d, "missing.gguf")
+        gguf_writer.write_gguf(gone, "mistral3", cfg, missing, types)
+        with pytest.raises(shs.TensorNotFoundError):
+            shs.MinistralModel.open(gone)
+
+
+def test_one_full_size_decoder_layer_t512(shs, oracle):
+    """One decoder layer at T=512 on X ~ N(0,1): RMSNorm (gain N(1,0.1)), Q4_0 q/k/v, RoPE θ=1e6,
+    GQA 32/8, o-proj + residual, RMSNorm, SwiGLU FFN 9216 + residual."""
+    cfg = oracle.make_config(n_layer=1, vocab=64)
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=33)
+    gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types)
+    x = np.random.default_rng(34).standard_normal((512, 3072)).astype(np.float32)
+    y = gpu.layer_forward(0, x)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=512)
+    ref = ora.layer_forward(0, x)
+    assert H.rel_l2(y, ref) < FP_TOL, H.rel_l2(y, ref)
+    assert H.max_close(y, ref) < 1e-3
+    gpu.close()
+
+
+def test_synthetic_model_round_trips_through_download(shs, oracle):
+    cfg = oracle.make_config(n_layer=2, hidden=256, n_head=8, n_kv_head=2, ffn=768, vocab=1000)
+    scfg = H.shs_config_from_oracle(shs, cfg)
+    syn = shs.MinistralModel.synthetic(scfg, shs.Q5_1, shs.Q4_0, seed=5)
+    names = list(scfg.tensor_shapes(shs.Q5_1, shs.Q4_0))
+    tensors = {n: syn.download(n) for n in names}
+    types = {n: (0 if n.endswith("norm.weight") else (2 if n == "token_embd.weight" else 7)) for n in names}
+    w = oracle.dequantize(7, tensors["blk.0.ffn_gate.weight"], 768 * 256)
+    assert abs(float(np.std(w)) - 0.02) < 0.002 and abs(float(np.mean(w))) < 0.002
+    g = tensors["blk.1.attn_norm.weight"]
+    assert abs(float(np.mean(g)) - 1.0) < 0.03 and abs(float(np.std(g)) - 0.1) < 0.03
+    again = shs.MinistralModel.from_tensors(scfg, tensors, types)
+    toks = np.random.default_rng(10).integers(0, cfg.vocab, 64)
+    a = syn.forward(toks)
+    b = again.forward(toks)
+    assert np.array_equal(a, b)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=64)
+    assert H.rel_l2(a, ora.forward(toks, head_mode=2)) < FP_TOL
+    syn.close()
+    again.close()
