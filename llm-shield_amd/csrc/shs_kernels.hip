@@ -686,11 +686,12 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     const AttnItem it = items[n_items - 1 - blockIdx.x];
     const int kvh = blockIdx.y;
     const int group = n_head / n_kv;
-    const int head = kvh * group + wave;
+    const bool active = wave < group;  // blocks have 4 waves; groups of < 4 heads idle the rest
+    const int head = active ? kvh * group + wave : kvh * group;
     const float* kb = kc + (int64_t)kvh * cap * ATT_HD;
     const float* vb = vc + (int64_t)kvh * cap * ATT_HD;
 
-    const bool qvalid = j < it.q_count;
+    const bool qvalid = active && j < it.q_count;
     float qr[64];
     {
         const float* qrow = q + (int64_t)(it.q_start + (qvalid ? j : 0)) * ldq + head * ATT_HD + 64 * h;
@@ -725,7 +726,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
             *reinterpret_cast<float4*>(&Vs[key * ATT_HD + 4 * d4]) = vv;
         }
         __syncthreads();
-        if (group <= wave) continue;
+        if (!active) continue;
 
         v16f s;
         for (int r = 0; r < 16; r++) s[r] = 0.0f;
@@ -761,7 +762,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * ATT_HD + 32 * dt + j], p[c], o[dt], 0, 0, 0);
             }
     }
-    if (!qvalid || wave >= group) return;
+    if (!qvalid) return;
     float* out = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD;
     for (int dt = 0; dt < 4; dt++)
         for (int g = 0; g < 4; g++) {
