@@ -75,7 +75,6 @@ def main():
         return 2
 
     import numpy as np
-    import torch
     import shieldstral as S
 
     cfg = S.SHIELDSTRAL_3B
@@ -93,13 +92,16 @@ def main():
 
     for _ in range(args.warmup):
         step()
+    # Every library call returns only after its stream has drained, so the region is
+    # bracketed by device synchronisation on both sides. torch is not imported: it
+    # bundles its own HIP/HSA runtime, and two HSA runtimes cannot share one process.
     model.profile_reset()
     model.profile(True)
-    torch.cuda.synchronize()
+    model.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         result = step()
-    torch.cuda.synchronize()
+    model.synchronize()
     elapsed = time.perf_counter() - t0
     model.profile(False)
     ms = elapsed / args.steps * 1e3

@@ -169,6 +169,9 @@ shs_status shs_matmul_block_sums(shs_matrix* m, const float* x, int32_t tokens, 
  * stream and returns when the result is written. */
 shs_status shs_matmul_device(shs_matrix* m, const float* x_dev, int32_t tokens, float* y_dev);
 
+/* Blocks until every operation queued on the model's stream has completed. */
+shs_status shs_synchronize(shs_model* model);
+
 /* --------------------------------------------------------------- timing */
 
 /* Per-kernel-class timing with HIP events recorded on the launching stream around

@@ -1180,6 +1180,14 @@ extern "C" shs_status shs_layer_forward(shs_model* m, int32_t layer, const float
     return SHS_OK;
 }
 
+extern "C" shs_status shs_synchronize(shs_model* m)
+{
+    if (!m) return fail(SHS_E_INVALID_ARGUMENT, "null model");
+    HIP_TRY(hipSetDevice(m->device));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
 // --------------------------------------------------------------- profiling
 
 extern "C" shs_status shs_profile_enable(shs_model* m, int32_t enable)

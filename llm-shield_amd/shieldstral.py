@@ -103,7 +103,7 @@ EXPORTS = (
     "shs_get_config", "shs_kv_reset", "shs_kv_length", "shs_kv_capacity", "shs_kv_snapshot", "shs_kv_restore",
     "shs_forward", "shs_forward_batch", "shs_set_capture", "shs_layer_forward", "shs_matrix_create",
     "shs_matrix_free", "shs_matmul", "shs_matmul_rows", "shs_matmul_block_sums", "shs_matmul_device",
-    "shs_profile_enable", "shs_profile_read", "shs_profile_reset",
+    "shs_profile_enable", "shs_profile_read", "shs_profile_reset", "shs_synchronize",
 )
 
 _lib = None
@@ -152,6 +152,7 @@ def _declare(L: C.CDLL) -> None:
         "shs_profile_enable": [P, I32],
         "shs_profile_read": [P, C.c_char_p, C.POINTER(I64), C.POINTER(C.c_double), C.POINTER(C.c_double)],
         "shs_profile_reset": [P],
+        "shs_synchronize": [P],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -508,6 +509,10 @@ class MinistralModel:
         y = np.empty_like(x)
         _check(_lib.shs_layer_forward(self._h, layer, _ptr(x), x.shape[0], _ptr(y)))
         return y
+
+    def synchronize(self) -> None:
+        """Waits until all work queued on the model's stream has finished."""
+        _check(_lib.shs_synchronize(self._h))
 
     # kernel-class timing (HIP events on the model's stream)
     def profile(self, enable: bool) -> None:

@@ -103,13 +103,22 @@ def test_a_row_subset_rejects_ids_outside_the_matrix(lib, oracle):
 
 
 def test_device_pointer_entry_matches_host_entry(lib, oracle):
-    import torch
+    """Activations already in HBM (allocated with the HIP runtime the library uses)."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")
     rows, cols, T = 256, 1024, 70
     w = H.random_blocks(2, rows, cols, seed=9)
     x = np.random.default_rng(9).standard_normal((T, cols)).astype(np.float32)
     m = lib.WeightMatrix(2, rows, cols, w)
-    xd = torch.from_numpy(x).cuda()
-    yd = torch.empty((T, rows), dtype=torch.float32, device="cuda")
-    torch.cuda.synchronize()
-    m.forward_device(xd.data_ptr(), T, yd.data_ptr())
-    assert np.array_equal(yd.cpu().numpy(), m.forward(x))
+    xd, yd = C.c_void_p(), C.c_void_p()
+    assert hip.hipMalloc(C.byref(xd), C.c_size_t(x.nbytes)) == 0
+    assert hip.hipMalloc(C.byref(yd), C.c_size_t(T * rows * 4)) == 0
+    try:
+        assert hip.hipMemcpy(xd, x.ctypes.data_as(C.c_void_p), C.c_size_t(x.nbytes), 1) == 0
+        m.forward_device(xd.value, T, yd.value)
+        y = np.empty((T, rows), np.float32)
+        assert hip.hipMemcpy(y.ctypes.data_as(C.c_void_p), yd, C.c_size_t(y.nbytes), 2) == 0
+    finally:
+        hip.hipFree(xd)
+        hip.hipFree(yd)
+    assert np.array_equal(y, m.forward(x))
