@@ -338,10 +338,52 @@ __device__ inline v4i load_weights(const uint8_t* __restrict__ wqs, const uint32
     }
 }
 
+// Operands of one 32-wide quant block for one wave: the 32-row weight tile and TT token tiles.
+template <int TT> struct GemmOps {
+    v4i w;
+    float4 d[4], m[4];
+    v4i x[TT];
+    float da[TT], ds[TT];
+};
+
+template <int TYPE, int TT>
+__device__ __forceinline__ void gemm_load(GemmOps<TT>& o, const uint8_t* __restrict__ wqs,
+                                          const uint32_t* __restrict__ wqh, const float* __restrict__ wd,
+                                          const float* __restrict__ wm, const ActQ8& a, int rt, int B, int b,
+                                          int tt0, int nv, int j, int h)
+{
+    constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
+    const int64_t rec = (int64_t)rt * B + b;
+    o.w = load_weights<TYPE>(wqs, wqh, rec, j, h);
+    const float4* dp = reinterpret_cast<const float4*>(wd + rec * 32);
+#pragma unroll
+    for (int g = 0; g < 4; g++) o.d[g] = dp[2 * g + h];
+    if (OFF) {
+        const float4* mp = reinterpret_cast<const float4*>(wm + rec * 32);
+#pragma unroll
+        for (int g = 0; g < 4; g++) o.m[g] = mp[2 * g + h];
+    }
+#pragma unroll
+    for (int u = 0; u < TT; u++) {
+        if (u < nv) {
+            const int tile = tt0 + u;
+            o.x[u] = *reinterpret_cast<const v4i*>(a.q + ((int64_t)tile * B + b) * 1024 + j * 32 + h * 16);
+            o.da[u] = a.d[(int64_t)b * a.Tpad + tile * 32 + j];
+            if (OFF) o.ds[u] = a.ds[(int64_t)b * a.Tpad + tile * 32 + j];
+        }
+    }
+}
+
+__device__ __forceinline__ float f4get(const float4& v, int k)
+{
+    return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
+}
+
 // One wave: a 32-row tile × TT 32-token tiles, K consumed one 32-wide quant block per
 // v_mfma_i32_32x32x32_i8. D[i][j] (row i, token j) sits in lane j + 32·(i%8 / 4), register
 // 4·(i/8) + i%4. Each output then takes, block by block in order, exactly the reference's
 // acc = fma(float(I), RN(d_w·d_a), acc) (+ fma(m_w, RN(d_a·Σq), acc) for offset types).
+// The next block's operands are loaded into registers while the current block computes.
 template <int TYPE, int TT, int MODE>
 __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                               const float* __restrict__ wd, const float* __restrict__ wm,
@@ -358,49 +400,41 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
     nv = nv < TT ? nv : TT;
 
     v16f acc[TT];
+#pragma unroll
     for (int u = 0; u < TT; u++)
+#pragma unroll
         for (int r = 0; r < 16; r++) acc[u][r] = 0.0f;
     const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
+    GemmOps<TT> cur, nxt;
+    gemm_load<TYPE, TT>(cur, wqs, wqh, wd, wm, a, rt, B, 0, tt0, nv, j, h);
     for (int b = 0; b < B; ++b) {
-        const int64_t rec = (int64_t)rt * B + b;
-        const v4i wv = load_weights<TYPE>(wqs, wqh, rec, j, h);
-        float dw[16], mw[16];
-        const float4* dp = reinterpret_cast<const float4*>(wd + rec * 32);
-        for (int g = 0; g < 4; g++) {
-            float4 v = dp[2 * g + h];
-            dw[4 * g] = v.x; dw[4 * g + 1] = v.y; dw[4 * g + 2] = v.z; dw[4 * g + 3] = v.w;
-        }
-        if (OFF) {
-            const float4* mp = reinterpret_cast<const float4*>(wm + rec * 32);
-            for (int g = 0; g < 4; g++) {
-                float4 v = mp[2 * g + h];
-                mw[4 * g] = v.x; mw[4 * g + 1] = v.y; mw[4 * g + 2] = v.z; mw[4 * g + 3] = v.w;
-            }
-        }
+        if (b + 1 < B) gemm_load<TYPE, TT>(nxt, wqs, wqh, wd, wm, a, rt, B, b + 1, tt0, nv, j, h);
+#pragma unroll
         for (int u = 0; u < TT; u++) {
-            if (u >= nv) break;
-            const int tile = tt0 + u;
-            const v4i xv = *reinterpret_cast<const v4i*>(a.q + ((int64_t)tile * B + b) * 1024 + j * 32 + h * 16);
-            const float da = a.d[(int64_t)b * a.Tpad + tile * 32 + j];
-            const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(wv, xv, zero, 0, 0, 0);
-            for (int r = 0; r < 16; r++) {
-                float sc = dw[r] * da;
-                acc[u][r] = fmaf((float)D[r], sc, acc[u][r]);
-            }
-            if (OFF) {
-                const float dsv = a.ds[(int64_t)b * a.Tpad + tile * 32 + j];
-                for (int r = 0; r < 16; r++) acc[u][r] = fmaf(mw[r], dsv, acc[u][r]);
+            if (u < nv) {
+                const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.w, cur.x[u], zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float sc = f4get(cur.d[r >> 2], r & 3) * cur.da[u];
+                    acc[u][r] = fmaf((float)D[r], sc, acc[u][r]);
+                }
+                if (OFF) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[u][r] = fmaf(f4get(cur.m[r >> 2], r & 3), cur.ds[u], acc[u][r]);
+                }
             }
         }
+        cur = nxt;
     }
 
     const bool vec = ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
+#pragma unroll
     for (int u = 0; u < TT; u++) {
-        if (u >= nv) break;
         const int token = (tt0 + u) * 32 + j;
-        if (token >= a.T) continue;
+        if (u >= nv || token >= a.T) continue;
         float* yr = y + (int64_t)token * ldy;
+#pragma unroll
         for (int g = 0; g < 4; g++) {
             const int row = rt * 32 + 8 * g + 4 * h;
             if (vec && row + 3 < N) {
@@ -412,11 +446,13 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
                 }
                 *p = v;
             } else {
+#pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    if (row + k >= N) break;
-                    float v = acc[u][4 * g + k];
-                    if (MODE == GEMM_ADD) v = yr[row + k] + v;
-                    yr[row + k] = v;
+                    if (row + k < N) {
+                        float v = acc[u][4 * g + k];
+                        if (MODE == GEMM_ADD) v = yr[row + k] + v;
+                        yr[row + k] = v;
+                    }
                 }
             }
         }
