@@ -169,6 +169,11 @@ shs_status shs_matmul_block_sums(shs_matrix* m, const float* x, int32_t tokens, 
  * stream and returns when the result is written. */
 shs_status shs_matmul_device(shs_matrix* m, const float* x_dev, int32_t tokens, float* y_dev);
 
+/* e^x as the attention softmax and SwiGLU's sigmoid evaluate it on the device, for
+ * x[0..n) → y (host buffers). Parity instrumentation: the CPU restatement performs the
+ * same sequence of IEEE operations, and this entry lets a test compare them directly. */
+shs_status shs_debug_expf(const float* x, int32_t n, float* y, int32_t device);
+
 /* Blocks until every operation queued on the model's stream has completed. */
 shs_status shs_synchronize(shs_model* model);
 

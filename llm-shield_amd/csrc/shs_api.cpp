@@ -331,7 +331,7 @@ struct shs_model {
     int rope_cap = 0;
     Buf cos_tab, sin_tab, qscale_tab;
     // Work buffers, grown on demand.
-    Buf h, qkv, ctx, gu, tmp, normed, ffn_act, tokens, pos, items, ids, logits, last_rows, lastidx, bkc, bvc;
+    Buf h, qkv, ctx, gu, tmp, normed, ffn_act, tokens, pos, items, ids, logits, last_rows, lastidx, bkc, bvc, scores;
     ActBuf act;
     shs_capture_fn cap_fn = nullptr;
     void* cap_user = nullptr;
@@ -937,7 +937,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         {
             Timed tm(m->prof, "attention", 0, m->stream);
             HIP_TRY(launch_attention(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, c.head_dim,
-                                     scale, ctx, qdim, m->stream));
+                                     scale, ctx, qdim, m->scores.as<float>(), m->stream));
         }
         snprintf(name, sizeof name, "blk.%d.attn_weighted", l);
         if (cap_on && cp.observe(name, ctx, qdim, T, qdim) != SHS_OK) return SHS_E_DEVICE;
@@ -1032,8 +1032,24 @@ shs_status check_ids(const int32_t* ids, int n, int limit, const char* what)
 std::vector<AttnItem> causal_items(int q_begin, int n, int key_start, int pos0)
 {
     std::vector<AttnItem> v;
-    for (int k = 0; k * 32 < n; k++) v.push_back({q_begin + 32 * k, std::min(32, n - 32 * k), key_start, pos0 + 32 * k});
+    for (int k = 0; k * 32 < n; k++) v.push_back({q_begin + 32 * k, std::min(32, n - 32 * k), key_start, pos0 + 32 * k, 0});
     return v;
+}
+
+// Gives every item its own region of the score scratch (4 waves per KV head, one
+// 32×32 tile of 1024 floats per key tile) and makes sure the scratch is large enough.
+shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
+{
+    int64_t off = 0;
+    for (auto& it : items) {
+        it.s_off = off;
+        int64_t n_kt = (it.pos0 + it.q_count + 31) / 32;
+        off += n_kt * 1024 * (int64_t)m->cfg.n_kv_head * 4;
+    }
+    HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off, 1)));
+    HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
+    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
+    return SHS_OK;
 }
 
 }  // namespace
@@ -1061,10 +1077,9 @@ extern "C" shs_status shs_forward(shs_model* m, const int32_t* tokens, int32_t n
     std::vector<int32_t> pos(n);
     for (int t = 0; t < n; t++) pos[t] = start + t;
     std::vector<AttnItem> items = causal_items(0, n, 0, start);
-    HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
+    if ((st = place_items(m, items)) != SHS_OK) return st;
     HIP_TRY(hipMemcpyAsync(m->tokens.p, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
     HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
     if (head_mode == 1) {
         HIP_TRY(m->ids.ensure(sizeof(int32_t) * n_ids));
         HIP_TRY(hipMemcpyAsync(m->ids.p, vocab_ids, sizeof(int32_t) * n_ids, hipMemcpyHostToDevice, m->stream));
@@ -1128,11 +1143,10 @@ extern "C" shs_status shs_forward_batch(shs_model* m, const int32_t* tokens, con
     // The kernel takes items from the back: put the longest key ranges there.
     std::stable_sort(items.begin(), items.end(),
                      [](const AttnItem& x, const AttnItem& y) { return x.pos0 + x.q_count < y.pos0 + y.q_count; });
-    HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
+    if ((st = place_items(m, items)) != SHS_OK) return st;
     HIP_TRY(m->ids.ensure(sizeof(int32_t) * n_ids));
     HIP_TRY(hipMemcpyAsync(m->tokens.p, tokens, sizeof(int32_t) * T, hipMemcpyHostToDevice, m->stream));
     HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * T, hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
     HIP_TRY(hipMemcpyAsync(m->ids.p, vocab_ids, sizeof(int32_t) * n_ids, hipMemcpyHostToDevice, m->stream));
     {
         Timed tm(m->prof, "embed", 0, m->stream);
@@ -1167,9 +1181,8 @@ extern "C" shs_status shs_layer_forward(shs_model* m, int32_t layer, const float
     std::vector<int32_t> pos(n);
     for (int t = 0; t < n; t++) pos[t] = t;
     std::vector<AttnItem> items = causal_items(0, n, 0, 0);
-    HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
+    if ((st = place_items(m, items)) != SHS_OK) return st;
     HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
     HIP_TRY(hipMemcpyAsync(m->h.p, x, sizeof(float) * (size_t)n * c.hidden, hipMemcpyHostToDevice, m->stream));
     m->len = 0;
     st = run_layers(m, n, m->kc, m->vc, m->cap, 0, layer, layer + 1, m->items.as<AttnItem>(), (int)items.size(), nullptr, true);
@@ -1185,6 +1198,21 @@ extern "C" shs_status shs_synchronize(shs_model* m)
     if (!m) return fail(SHS_E_INVALID_ARGUMENT, "null model");
     HIP_TRY(hipSetDevice(m->device));
     HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
+extern "C" shs_status shs_debug_expf(const float* x, int32_t n, float* y, int32_t device)
+{
+    if (!x || !y || n < 0) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    shs_status st = select_device(device);
+    if (st != SHS_OK) return st;
+    float* d = nullptr;
+    HIP_TRY(hipMalloc(&d, sizeof(float) * 2 * (size_t)std::max(n, 1)));
+    hipError_t e = hipMemcpy(d, x, sizeof(float) * n, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = launch_expf(d, n, d + n, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(y, d + n, sizeof(float) * n, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return hip_fail(e, "shs_debug_expf");
     return SHS_OK;
 }
 

@@ -40,9 +40,11 @@ struct ActQ8 {
 
 // Work item of the attention kernel: queries [q_start, q_start+q_count) of one
 // sequence, whose first query sits at position pos0 and whose keys live at cache
-// index key_start + p for p in [0, pos0 + q_count).
+// index key_start + p for p in [0, pos0 + q_count). Scores of the item's heads go to
+// scratch + s_off.
 struct AttnItem {
     int q_start, q_count, key_start, pos0;
+    int64_t s_off;  // this item's float offset in the score scratch (n_head · n_tiles · 1024 floats)
 };
 
 enum GemmMode { GEMM_STORE = 0, GEMM_ADD = 1 };
@@ -69,7 +71,8 @@ hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv_
                              int kv_slot0, hipStream_t s);
 hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap,
                             const AttnItem* items, int n_items, int n_head, int n_kv_head, int head_dim,
-                            float scale, float* ctx, int ldc, hipStream_t s);
+                            float scale, float* ctx, int ldc, float* scratch, hipStream_t s);
+hipError_t launch_expf(const float* x, int n, float* y, hipStream_t s);
 hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s);
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);
 hipError_t launch_add_inplace(float* a, const float* b, size_t n, hipStream_t s);

@@ -254,6 +254,8 @@ hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float e
     return hipGetLastError();
 }
 
+__device__ __forceinline__ float det_expf(float x);
+
 // ------------------------------------------------------- SwiGLU + quantize
 
 // Kernels.SwiGlu (Kernels.cs:83-90): gu = g·u, s = 1/(1+e^−g), y = s·gu; then the
@@ -270,7 +272,7 @@ __global__ void k_swiglu_quant(const float* __restrict__ gu, int ldgu, int ffn, 
     for (int k = 0; k < 32; k++) {
         float gv = g[k];
         float prod = gv * u[k];
-        float sg = 1.0f / (1.0f + expf(-gv));
+        float sg = 1.0f / (1.0f + det_expf(-gv));
         v[k] = sg * prod;
     }
     if (y_opt) {
@@ -703,119 +705,235 @@ hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv,
 
 // ------------------------------------------------------------------ attention
 
-// Causal GQA attention (MinistralModel.AttendGroup, MinistralModel.cs:372-440) as an
-// online-softmax pass over 32-key tiles. A block holds the 4 query heads of one KV head
-// for ≤32 queries; K (transposed) and V tiles are staged in LDS once for all four.
-// Scores S^T = K·Q^T and context O^T = V^T·P^T run on v_mfma_f32_32x32x2f32 (fp32
-// products, fp32 accumulation): lane j (query) holds 16 keys / 16 dims per tile.
+// e^x as a fixed sequence of IEEE single operations (Cody–Waite reduction with a
+// 16-bit head of ln 2, the degree-7 Taylor polynomial of e^r in fused Horner form,
+// exact scaling by 2^n), so that any implementation performing the same steps — the
+// CPU restatement included — returns the same bits. ≤ 1 ulp against float64 exp.
+__device__ __forceinline__ float det_expf(float x)
+{
+    if (x != x) return x;
+    if (!(x > -104.0f)) return 0.0f;
+    if (x > 0x1.62e42ep+6f) return INFINITY;
+    const float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-n, 0x1.62e400p-1f, x);
+    r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0x1p-1f);
+    p = fmaf(p, r, 0x1p+0f);
+    p = fmaf(p, r, 0x1p+0f);
+    return ldexpf(p, (int)n);
+}
+
+// Causal GQA attention in MinistralModel.AttendGroup's floating-point order
+// (MinistralModel.cs:372-440, Kernels.cs:103-220), bit for bit:
+//  * score = (Σ over 8 lanes of a 16-step FMA chain q[l+8m]·k[l+8m], summed pairwise)·scale
+//    — Kernels.Dot4 with Vector<float>.Count = 8;
+//  * softmax: max, e = exp(s − max), Σe over 8 strided lanes (pairwise) then the tail in
+//    order, w = e / Σe;
+//  * ctx[d] = fma(v[p][d], w[p], ctx[d]) for p = 0, 1, 2, … — Kernels.AddScaled4.
+// v_mfma_f32_32x32x2f32 computes fma(a1, b1, fma(a0, b0, c)) per element, so each
+// instruction is two consecutive steps of those FMA chains for a 32×32 tile. A block holds
+// the 4 query heads of one KV head for ≤ 32 queries; K and V tiles are staged in LDS.
+// Three passes over the keys: scores (kept in a scratch buffer) and their max; the sum of
+// exponentials; the weighted values. The score tile's rows are keys permuted so that lane
+// half h holds the keys of parity h, which lets the value pass consume register c of both
+// halves as the key pair (2c, 2c+1).
 constexpr int ATT_HD = 128;
 
 __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, int cap,
                                                    const AttnItem* __restrict__ items, int n_items, int n_head,
-                                                   int n_kv, float scale, float* __restrict__ ctx, int ldc)
+                                                   int n_kv, float scale, float* __restrict__ ctx, int ldc,
+                                                   float* __restrict__ scratch)
 {
-    __shared__ float Ks[ATT_HD * 32];
-    __shared__ float Vs[32 * ATT_HD];
+    __shared__ float Ks[ATT_HD * 32];  // [element][key]
+    __shared__ float Vs[32 * ATT_HD];  // [key][dim]
+    __shared__ float tail[4][32][8];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 31, h = lane >> 5;
     const AttnItem it = items[n_items - 1 - blockIdx.x];
     const int kvh = blockIdx.y;
     const int group = n_head / n_kv;
-    const bool active = wave < group;  // blocks have 4 waves; groups of < 4 heads idle the rest
+    const bool active = wave < group;
     const int head = active ? kvh * group + wave : kvh * group;
     const float* kb = kc + (int64_t)kvh * cap * ATT_HD;
     const float* vb = vc + (int64_t)kvh * cap * ATT_HD;
+    const int n_keys = it.pos0 + it.q_count;
+    const int n_kt = (n_keys + 31) >> 5;
+    float* sw = scratch + it.s_off + (int64_t)(kvh * 4 + wave) * n_kt * 1024;
 
     const bool qvalid = active && j < it.q_count;
-    float qr[64];
+    const int nq = it.pos0 + j + 1;  // keys this query attends to
+    // Query elements for the score chains: qv[8l + s] = q[l + 16s + 8h].
+    float qv[64];
     {
-        const float* qrow = q + (int64_t)(it.q_start + (qvalid ? j : 0)) * ldq + head * ATT_HD + 64 * h;
-        for (int c = 0; c < 64; c += 4) {
-            float4 v = qvalid ? *reinterpret_cast<const float4*>(qrow + c) : make_float4(0.f, 0.f, 0.f, 0.f);
-            qr[c] = v.x; qr[c + 1] = v.y; qr[c + 2] = v.z; qr[c + 3] = v.w;
-        }
+        const float* qrow = q + (int64_t)(it.q_start + (qvalid ? j : 0)) * ldq + head * ATT_HD;
+#pragma unroll
+        for (int l = 0; l < 8; l++)
+#pragma unroll
+            for (int s = 0; s < 8; s++) qv[8 * l + s] = qvalid ? qrow[l + 16 * s + 8 * h] : 0.0f;
     }
-    float m_run = -INFINITY, l_run = 0.0f;
-    v16f o[4];
-    for (int dt = 0; dt < 4; dt++)
-        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+    // Score row i of a tile holds key kap(i) = 8(i/8) + 2(i%4) + (i%8)/4.
+    const int kap = 8 * (j >> 3) + 2 * (j & 3) + ((j >> 2) & 1);
 
-    const int n_keys = it.pos0 + it.q_count;
-    const int qpos = it.pos0 + j;
-    const int n_kt = (n_keys + 31) >> 5;
+    // ---- pass 1: scores and their max
+    float mx = -INFINITY;
     for (int kt = 0; kt < n_kt; ++kt) {
         __syncthreads();
         for (int e = threadIdx.x; e < 32 * 32; e += blockDim.x) {
             const int key = e & 31, d4 = e >> 5;
             const int kidx = kt * 32 + key;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (kidx < n_keys) {
-                const int64_t off = (int64_t)(it.key_start + kidx) * ATT_HD + 4 * d4;
-                kv = *reinterpret_cast<const float4*>(kb + off);
-                vv = *reinterpret_cast<const float4*>(vb + off);
-            }
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (kidx < n_keys) kv = *reinterpret_cast<const float4*>(kb + (int64_t)(it.key_start + kidx) * ATT_HD + 4 * d4);
             Ks[(4 * d4 + 0) * 32 + key] = kv.x;
             Ks[(4 * d4 + 1) * 32 + key] = kv.y;
             Ks[(4 * d4 + 2) * 32 + key] = kv.z;
             Ks[(4 * d4 + 3) * 32 + key] = kv.w;
+        }
+        __syncthreads();
+        if (!active) continue;
+        v16f acc01, acc23, acc45, acc67;
+#pragma unroll
+        for (int pair = 0; pair < 4; pair++) {
+            v16f c0, c1;
+#pragma unroll
+            for (int r = 0; r < 16; r++) { c0[r] = 0.0f; c1[r] = 0.0f; }
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                const int l0 = 2 * pair, l1 = 2 * pair + 1;
+                c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(l0 + 16 * s + 8 * h) * 32 + kap], qv[8 * l0 + s], c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(l1 + 16 * s + 8 * h) * 32 + kap], qv[8 * l1 + s], c1, 0, 0, 0);
+            }
+            v16f sum;
+#pragma unroll
+            for (int r = 0; r < 16; r++) sum[r] = c0[r] + c1[r];
+            if (pair == 0) acc01 = sum;
+            else if (pair == 1) acc23 = sum;
+            else if (pair == 2) acc45 = sum;
+            else acc67 = sum;
+        }
+        float sc[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float a = acc01[r] + acc23[r];
+            const float b = acc45[r] + acc67[r];
+            sc[r] = (a + b) * scale;
+            const int key = kt * 32 + 8 * (r >> 2) + 2 * (r & 3) + h;
+            if (qvalid && key < nq) mx = fmaxf(mx, sc[r]);
+        }
+        float4* out = reinterpret_cast<float4*>(sw + ((int64_t)kt * 64 + lane) * 16);
+#pragma unroll
+        for (int g = 0; g < 4; g++) out[g] = make_float4(sc[4 * g], sc[4 * g + 1], sc[4 * g + 2], sc[4 * g + 3]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+
+    // ---- pass 2: Σ exp(s − max) over 8 strided lanes, pairwise, then the tail in order
+    const int n8 = nq & ~7;
+    float L[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // residues 2t + h
+    if (active) {
+        for (int kt = 0; kt < n_kt; ++kt) {
+            const float4* in = reinterpret_cast<const float4*>(sw + ((int64_t)kt * 64 + lane) * 16);
+            float sc[16];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 v = in[g];
+                sc[4 * g] = v.x; sc[4 * g + 1] = v.y; sc[4 * g + 2] = v.z; sc[4 * g + 3] = v.w;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int key = kt * 32 + 8 * (r >> 2) + 2 * (r & 3) + h;
+                if (!qvalid || key >= nq) continue;
+                const float e = det_expf(sc[r] - mx);
+                if (key < n8) L[r & 3] = L[r & 3] + e;
+                else tail[wave][j][key - n8] = e;
+            }
+        }
+    }
+    float other[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) other[t] = __shfl_xor(L[t], 32);
+    float a8[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        a8[2 * t] = h == 0 ? L[t] : other[t];
+        a8[2 * t + 1] = h == 0 ? other[t] : L[t];
+    }
+    float total = ((a8[0] + a8[1]) + (a8[2] + a8[3])) + ((a8[4] + a8[5]) + (a8[6] + a8[7]));
+    __syncthreads();
+    if (qvalid)
+        for (int p = 0; p < nq - n8; p++) total = total + tail[wave][j][p];
+
+    // ---- pass 3: ctx = Σ_p fma(v[p], w[p], ctx) in position order
+    v16f o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+    for (int kt = 0; kt < n_kt; ++kt) {
+        __syncthreads();
+        for (int e = threadIdx.x; e < 32 * 32; e += blockDim.x) {
+            const int key = e & 31, d4 = e >> 5;
+            const int kidx = kt * 32 + key;
+            float4 vv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (kidx < n_keys) vv = *reinterpret_cast<const float4*>(vb + (int64_t)(it.key_start + kidx) * ATT_HD + 4 * d4);
             *reinterpret_cast<float4*>(&Vs[key * ATT_HD + 4 * d4]) = vv;
         }
         __syncthreads();
         if (!active) continue;
-
-        v16f s;
-        for (int r = 0; r < 16; r++) s[r] = 0.0f;
-        for (int c = 0; c < 64; ++c)
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(64 * h + c) * 32 + j], qr[c], s, 0, 0, 0);
-
-        float p[16];
-        float tmax = -INFINITY;
-        for (int r = 0; r < 16; r++) {
-            const int key = kt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            float sv = s[r] * scale;
-            if (key > qpos || !qvalid) sv = -INFINITY;
-            p[r] = sv;
-            tmax = fmaxf(tmax, sv);
+        const float4* in = reinterpret_cast<const float4*>(sw + ((int64_t)kt * 64 + lane) * 16);
+        float w[16];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 v = in[g];
+            w[4 * g] = v.x; w[4 * g + 1] = v.y; w[4 * g + 2] = v.z; w[4 * g + 3] = v.w;
         }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m_run, tmax);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = expf(m_run - m_use);
-        float rs = 0.0f;
+#pragma unroll
         for (int r = 0; r < 16; r++) {
-            p[r] = expf(p[r] - m_use);
-            rs += p[r];
+            const int key = kt * 32 + 8 * (r >> 2) + 2 * (r & 3) + h;
+            w[r] = (qvalid && key < nq) ? det_expf(w[r] - mx) / total : 0.0f;
         }
-        rs += __shfl_xor(rs, 32);
-        l_run = l_run * alpha + rs;
-        m_run = m_new;
-        for (int dt = 0; dt < 4; dt++)
-            for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
-        for (int dt = 0; dt < 4; dt++)
-            for (int c = 0; c < 16; c++) {
-                const int key = 8 * (c >> 2) + 4 * h + (c & 3);
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[key * ATT_HD + 32 * dt + j], p[c], o[dt], 0, 0, 0);
-            }
+#pragma unroll
+        for (int c = 0; c < 16; c++)
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(2 * c + h) * ATT_HD + 32 * dt + j], w[c], o[dt], 0, 0, 0);
     }
     if (!qvalid) return;
-    float* out = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD;
+    float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD;
+#pragma unroll
     for (int dt = 0; dt < 4; dt++)
+#pragma unroll
         for (int g = 0; g < 4; g++) {
             const int dim = 32 * dt + 8 * g + 4 * h;
-            float4 v = make_float4(o[dt][4 * g] / l_run, o[dt][4 * g + 1] / l_run, o[dt][4 * g + 2] / l_run,
-                                   o[dt][4 * g + 3] / l_run);
-            *reinterpret_cast<float4*>(out + dim) = v;
+            *reinterpret_cast<float4*>(outp + dim) =
+                make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
         }
 }
 
 hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
                             int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
-                            hipStream_t s)
+                            float* scratch, hipStream_t s)
 {
     if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_attention, dim3(n_items, n_kv), dim3(256), 0, s, q, ldq, kc, vc, cap, items, n_items, n_head,
-                       n_kv, scale, ctx, ldc);
+                       n_kv, scale, ctx, ldc, scratch);
+    return hipGetLastError();
+}
+
+__global__ void k_expf(const float* __restrict__ x, int n, float* __restrict__ y)
+{
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = det_expf(x[i]);
+}
+
+hipError_t launch_expf(const float* x, int n, float* y, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_expf, dim3((n + 255) / 256), dim3(256), 0, s, x, n, y);
     return hipGetLastError();
 }
 

@@ -104,6 +104,7 @@ EXPORTS = (
     "shs_forward", "shs_forward_batch", "shs_set_capture", "shs_layer_forward", "shs_matrix_create",
     "shs_matrix_free", "shs_matmul", "shs_matmul_rows", "shs_matmul_block_sums", "shs_matmul_device",
     "shs_profile_enable", "shs_profile_read", "shs_profile_reset", "shs_synchronize",
+    "shs_debug_expf",
 )
 
 _lib = None
@@ -153,6 +154,7 @@ def _declare(L: C.CDLL) -> None:
         "shs_profile_read": [P, C.c_char_p, C.POINTER(I64), C.POINTER(C.c_double), C.POINTER(C.c_double)],
         "shs_profile_reset": [P],
         "shs_synchronize": [P],
+        "shs_debug_expf": [P, I32, P, I32],
     }
     for name, args in sigs.items():
         fn = getattr(L, name)
@@ -525,6 +527,15 @@ class MinistralModel:
         n, ms, ops = C.c_int64(), C.c_double(), C.c_double()
         _check(_lib.shs_profile_read(self._h, kernel_class.encode(), C.byref(n), C.byref(ms), C.byref(ops)))
         return n.value, ms.value, ops.value
+
+
+def device_expf(x, device: int = 0) -> np.ndarray:
+    """The device's softmax/sigmoid exponential on x (parity instrumentation)."""
+    lib = load_library()
+    x = _arr(x, np.float32).reshape(-1)
+    y = np.empty_like(x)
+    _check(lib.shs_debug_expf(_ptr(x), x.size, _ptr(y), device))
+    return y
 
 
 class CancellationFlag:

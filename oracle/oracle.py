@@ -93,6 +93,8 @@ def _declare(L: C.CDLL) -> None:
     L.ora_forward.argtypes = [C.POINTER(Model), C.POINTER(KV), P, C.c_int, C.c_int, P, C.c_int, P,
                               CAPTURE_FN, P, C.c_int]
     L.ora_score.argtypes = [P, C.c_int, C.c_int, P, P, P]
+    L.ora_expf.argtypes = [C.c_float]
+    L.ora_expf.restype = C.c_float
     L.ora_layer_forward.argtypes = [C.POINTER(Model), C.POINTER(KV), C.c_int, P, C.c_int, P, C.c_int]
 
 

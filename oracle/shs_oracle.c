@@ -23,9 +23,13 @@
  *   ora_forward              numpy float64 restatement of one layer and of the model on
  *                            tiny shapes (1e-4 relative); prefix-cache bit identity
  *   ora_score                closed form
- * Parity unpinned at the ulp level: exp/sigmoid/cos/sin/pow come from glibc here and
- * from System.Numerics.Tensors / the .NET runtime in the reference; the order of the
- * horizontal Vector<float>.Sum is taken to be pairwise (((0+1)+(2+3))+((4+5)+(6+7))).
+ *   ora_expf                 float64 exp within 2 ulp over [-104, 89]; exact at 0; the
+ *                            overflow and underflow edges
+ * Parity unpinned at the ulp level against .NET: exp/sigmoid (ora_expf here, the
+ * vectorized polynomial of System.Numerics.Tensors there), cos/sin/pow (glibc here, the
+ * .NET runtime's CRT calls there), and the order of the horizontal Vector<float>.Sum
+ * (taken to be pairwise, ((0+1)+(2+3))+((4+5)+(6+7))) and of TensorPrimitives.Sum
+ * (taken to be 8 strided lanes, pairwise-summed, then the tail in order).
  */
 #include "shs_oracle.h"
 
@@ -552,6 +556,34 @@ void ora_rmsnorm(const float* x, const float* w, float eps, int n, float* y)
     for (i = 0; i < n; i++) y[i] = x[i] * scale * w[i];
 }
 
+/* e^x for TensorPrimitives.Exp/Sigmoid (Kernels.cs:88,120). The reference's vectorized
+ * exp is a polynomial of its own; this restatement fixes one: Cody–Waite reduction
+ * x = n·ln2 + r with ln2 split into a 16-bit head (so n·head is exact) and a tail,
+ * the degree-7 Taylor polynomial of e^r in Horner form with fused multiply-adds, and
+ * an exact scaling by 2^n. Every step is an IEEE single operation, so any
+ * implementation that performs the same steps returns the same bits. ≤ 2 ulp. */
+float ora_expf(float x)
+{
+    if (x != x) return x;
+    if (!(x > -104.0f)) return 0.0f;
+    if (x > 0x1.62e42ep+6f) return INFINITY;         /* ln(FLT_MAX) rounded down */
+    const float log2e = 0x1.715476p+0f;                /* RN(1/ln 2) */
+    const float ln2_hi = 0x1.62e400p-1f;               /* ln 2 to 16 significant bits */
+    const float ln2_lo = 0x1.7f7d1cp-20f;              /* RN(ln 2 − ln2_hi) */
+    float n = nearbyintf(x * log2e);
+    float r = fmaf(-n, ln2_hi, x);
+    r = fmaf(-n, ln2_lo, r);
+    float p = 0x1.a01a02p-13f;                         /* 1/7! */
+    p = fmaf(p, r, 0x1.6c16c2p-10f);                   /* 1/6! */
+    p = fmaf(p, r, 0x1.111112p-7f);                    /* 1/5! */
+    p = fmaf(p, r, 0x1.555556p-5f);                    /* 1/4! */
+    p = fmaf(p, r, 0x1.555556p-3f);                    /* 1/3! */
+    p = fmaf(p, r, 0x1p-1f);
+    p = fmaf(p, r, 0x1p+0f);
+    p = fmaf(p, r, 0x1p+0f);
+    return ldexpf(p, (int)n);
+}
+
 /* Kernels.SwiGlu (Kernels.cs:83-90): up ← g·u; dst ← sigmoid(g); dst ← dst·up. */
 void ora_swiglu(const float* gate, float* up, float* dst, int64_t n)
 {
@@ -559,7 +591,7 @@ void ora_swiglu(const float* gate, float* up, float* dst, int64_t n)
         float g = gate[i];
         float gu = g * up[i];
         up[i] = gu;
-        float sg = 1.0f / (1.0f + expf(-g));
+        float sg = 1.0f / (1.0f + ora_expf(-g));
         dst[i] = sg * gu;
     }
 }
@@ -577,7 +609,7 @@ void ora_softmax(float* x, int n)
     }
     float lanes[8] = {0};
     int i = 0;
-    for (; i < n; i++) x[i] = expf(x[i] - mx);
+    for (; i < n; i++) x[i] = ora_expf(x[i] - mx);
     for (i = 0; i + 8 <= n; i += 8)
         for (int l = 0; l < 8; l++) lanes[l] += x[i + l];
     float sum = vsum8(lanes);

@@ -1,10 +1,11 @@
 """The HIP forward pass (MinistralModel / ShieldstralModerator parity) against the oracle.
 
-Bars: stages that are integer or single IEEE ops (RMSNorm in the reference's order, the
-int8 quantization, the GEMM epilogue, RoPE from the same cos/sin) are compared
-bit-exactly where their inputs are; everything downstream of attention's exp/online
-softmax is held to relative L2 ≤ 1e-4 (the north-star fp32 tolerance), and the Score
-to 1e-4 absolute."""
+Bar: bit-exact. Every stage performs the reference's floating-point operations in the
+reference's order (RMSNorm's lane sums, the int8 quantization, the serial GEMM epilogue,
+RoPE from the same cos/sin, attention's Dot4 chains / softmax / AddScaled4 chain, the
+deterministic exp both sides share), so every captured tensor, the KV cache and the
+logits must match the oracle bit for bit. The Score is then identical too; the looser
+bounds kept below (1e-4) are the north-star tolerances, asserted as well."""
 import math
 import os
 import tempfile
@@ -44,11 +45,9 @@ def test_forward_matches_oracle_and_first_layer_is_bit_exact(shs, oracle, tiny):
     expected = {"embeddings", "final_norm", "logits"} | {
         f"blk.{l}.{s}" for l in range(cfg.n_layer) for s in H.CAPTURE_NAMES_PER_LAYER}
     assert set(gcap) == expected == set(ocap)
-    for name in ("embeddings", "blk.0.attn_norm", "blk.0.q_rope", "blk.0.k_rope", "blk.0.v"):
-        assert np.array_equal(gcap[name], ocap[name]), name
-    for name in expected:
-        assert H.rel_l2(gcap[name], ocap[name]) < FP_TOL, (name, H.rel_l2(gcap[name], ocap[name]))
-    assert H.rel_l2(g, o) < FP_TOL
+    for name in sorted(expected):
+        assert np.array_equal(gcap[name], ocap[name]), (name, H.rel_l2(gcap[name], ocap[name]))
+    assert np.array_equal(g, o)
 
 
 def test_selected_rows_are_bit_identical_to_the_full_head(shs, tiny):
@@ -87,9 +86,7 @@ def test_kv_snapshot_layout_matches_the_oracle(shs, tiny):
     snap = gpu.kv_cache.snapshot(45)
     ref = ora.snapshot(45)
     assert snap.shape == ref.shape
-    per = cfg.n_kv_head * 45 * cfg.head_dim  # layer 0 keys are bit-exact
-    assert np.array_equal(snap[:per], ref[:per])
-    assert H.rel_l2(snap, ref) < FP_TOL
+    assert np.array_equal(snap, ref)
     with pytest.raises(shs.ArgumentOutOfRangeError):
         gpu.kv_cache.snapshot(46)
     with pytest.raises(shs.ArgumentError):
@@ -147,7 +144,7 @@ def test_packed_ragged_batch_equals_one_prompt_at_a_time(shs, oracle, tiny):
         gpu.reset_kv_cache()
         assert np.array_equal(gpu.forward_selected(p, ids), row)
         ora.reset()
-        assert H.rel_l2(row, ora.forward(p, head_mode=1, vocab_ids=ids)) < FP_TOL
+        assert np.array_equal(row, ora.forward(p, head_mode=1, vocab_ids=ids))
 
 
 def test_moderator_scores_like_the_oracle(shs, oracle, tiny):
@@ -167,7 +164,8 @@ def test_moderator_scores_like_the_oracle(shs, oracle, tiny):
         ora.reset()
         logits = ora.forward(prompt, head_mode=1, vocab_ids=yes + no)
         s, y, n = oracle.score(logits, 3, 2)
-        assert abs(r.score - s) < 1e-4 and abs(r.yes_logit - y) < 1e-4 * max(1, abs(y))
+        assert r.yes_logit == y and r.no_logit == n
+        assert abs(r.score - s) < 1e-6
         assert r.is_unsafe == (r.score > 0.5) and r.is_unsafe_at(0.0) == (r.score > 0.0)
         other = rng.integers(0, cfg.vocab, 30)  # no shared prefix: the cache is reset, not restored
         r2 = mod.moderate_tokens(other)
@@ -219,8 +217,7 @@ def test_one_full_size_decoder_layer_t512(shs, oracle):
     y = gpu.layer_forward(0, x)
     ora = oracle.OracleModel(cfg, tensors, types, cap=512)
     ref = ora.layer_forward(0, x)
-    assert H.rel_l2(y, ref) < FP_TOL, H.rel_l2(y, ref)
-    assert H.max_close(y, ref) < 1e-3
+    assert np.array_equal(y, ref), H.rel_l2(y, ref)
     gpu.close()
 
 
@@ -241,6 +238,17 @@ def test_synthetic_model_round_trips_through_download(shs, oracle):
     b = again.forward(toks)
     assert np.array_equal(a, b)
     ora = oracle.OracleModel(cfg, tensors, types, cap=64)
-    assert H.rel_l2(a, ora.forward(toks, head_mode=2)) < FP_TOL
+    assert np.array_equal(a, ora.forward(toks, head_mode=2))
     syn.close()
     again.close()
+
+
+def test_device_exp_is_the_oracle_exp_bit_for_bit(shs, oracle):
+    rng = np.random.default_rng(12)
+    x = np.concatenate([np.linspace(-110, 90, 400001, dtype=np.float32),
+                        (rng.standard_normal(200000) * 30).astype(np.float32),
+                        np.array([0.0, -0.0, -104.0, -103.99, -87.5, 88.72, 88.73, np.inf, -np.inf], np.float32)])
+    got = shs.device_expf(x)
+    lib = oracle.lib()
+    ref = np.array([lib.ora_expf(float(v)) for v in x], np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
