@@ -81,14 +81,14 @@ struct ActBuf {
         int Tpad = (T + 31) / 32 * 32;
         int B = K / 32;
         hipError_t e;
-        if ((e = q.ensure((size_t)Tpad * K)) != hipSuccess) return e;
+        if ((e = q.ensure((size_t)Tpad * K * 2)) != hipSuccess) return e;
         if ((e = d.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
         if ((e = ds.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
         view->T = T;
         view->Tpad = Tpad;
         view->K = K;
         view->B = B;
-        view->q = q.as<int8_t>();
+        view->q = q.as<uint16_t>();
         view->d = d.as<float>();
         view->ds = ds.as<float>();
         return hipSuccess;

@@ -9,9 +9,10 @@
 //     d   [tiles][B][32 rows] f32   block scale, fp16 widened exactly
 //     m   [tiles][B][32 rows] f32   block min (Q4_1/Q5_1)
 // Quantized activations (T padded to Tpad, a multiple of 32):
-//     q   [Tpad/32][B][32 tokens][32 B]  int8, each block stored in the order
-//                                        [0..7, 16..23 | 8..15, 24..31] so MFMA lane half h
-//                                        reads bytes 16h..16h+15 (matches the weight nibbles)
+//     q   [Tpad/32][B][32 tokens][32 fp16]  the int8 values as exact fp16, each block stored
+//                                          in the order [0..7, 16..23, 8..15, 24..31] so MFMA
+//                                          lane half h reads elements 8h.. and 16+8h.. as two
+//                                          16-byte runs (matching the weight nibbles)
 //     d   [B][Tpad] f32   scale max|x|/127
 //     ds  [B][Tpad] f32   RN(d·float(Σq)) — the offset types' second factor
 #pragma once
@@ -33,7 +34,7 @@ struct DevMatrix {
 
 struct ActQ8 {
     int T = 0, Tpad = 0, K = 0, B = 0;
-    int8_t* q = nullptr;
+    uint16_t* q = nullptr;  // fp16 integer values
     float* d = nullptr;
     float* ds = nullptr;
 };

@@ -137,24 +137,25 @@ __device__ inline void quant32(const float* v, int semantics, int8_t* q, float& 
 
 __device__ inline void store_q8_block(const ActQ8& a, int t, int b, const int8_t* q, float dd, float ds)
 {
-    uint32_t w[8];
-    for (int p4 = 0; p4 < 8; p4++) {
-        uint32_t x = 0;
-        for (int k = 0; k < 4; k++) x |= (uint32_t)(uint8_t)q[perm_elem(4 * p4 + k)] << (8 * k);
-        w[p4] = x;
+    uint32_t w[16];
+    for (int p2 = 0; p2 < 16; p2++) {
+        const _Float16 x0 = (_Float16)(float)q[perm_elem(2 * p2)];
+        const _Float16 x1 = (_Float16)(float)q[perm_elem(2 * p2 + 1)];
+        w[p2] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
     }
-    int8_t* dst = a.q + ((int64_t)(t >> 5) * a.B + b) * 1024 + (t & 31) * 32;
-    reinterpret_cast<uint4*>(dst)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    reinterpret_cast<uint4*>(dst)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    uint4* dst = reinterpret_cast<uint4*>(a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    dst[2] = make_uint4(w[8], w[9], w[10], w[11]);
+    dst[3] = make_uint4(w[12], w[13], w[14], w[15]);
     a.d[(int64_t)b * a.Tpad + t] = dd;
     a.ds[(int64_t)b * a.Tpad + t] = ds;
 }
 
 __device__ inline void store_zero_block(const ActQ8& a, int t, int b)
 {
-    int8_t* dst = a.q + ((int64_t)(t >> 5) * a.B + b) * 1024 + (t & 31) * 32;
-    reinterpret_cast<uint4*>(dst)[0] = make_uint4(0, 0, 0, 0);
-    reinterpret_cast<uint4*>(dst)[1] = make_uint4(0, 0, 0, 0);
+    uint4* dst = reinterpret_cast<uint4*>(a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32);
+    for (int k = 0; k < 4; k++) dst[k] = make_uint4(0, 0, 0, 0);
     a.d[(int64_t)b * a.Tpad + t] = 0.0f;
     a.ds[(int64_t)b * a.Tpad + t] = 0.0f;
 }
@@ -294,141 +295,233 @@ hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& 
 
 // ------------------------------------------------------------------- GEMM
 
-// Four 4-bit fifth-bit flags → 0x10 in the byte of each set bit.
-__device__ inline uint32_t expand_bits4(uint32_t x4)
-{
-    return ((__umul24(x4, 0x00204081u)) & 0x01010101u) << 4;
-}
-
-// The 16 signed weights lane half h feeds the MFMA, from the row's 16 qs bytes (dwords
-// q0 = bytes 8h..8h+3, q1 = 8h+4..8h+7) and the fifth bits: register bytes are quant
-// elements [8h..8h+7, 16+8h..16+8h+7], i.e. w = u − z with z = 8 (Q4_0), 16 (Q5_0) or 0.
-template <int TYPE>
-__device__ inline v4i unpack_half(uint32_t q0, uint32_t q1, uint32_t qh, int h)
-{
-    uint32_t lo0 = q0 & 0x0F0F0F0Fu, lo1 = q1 & 0x0F0F0F0Fu;
-    uint32_t hi0 = (q0 >> 4) & 0x0F0F0F0Fu, hi1 = (q1 >> 4) & 0x0F0F0F0Fu;
-    if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) {
-        uint32_t sh = 8u * h;
-        lo0 |= expand_bits4((qh >> sh) & 0xFu);
-        lo1 |= expand_bits4((qh >> (sh + 4)) & 0xFu);
-        hi0 |= expand_bits4((qh >> (sh + 16)) & 0xFu);
-        hi1 |= expand_bits4((qh >> (sh + 20)) & 0xFu);
-    }
-    if (TYPE == SHS_TYPE_Q4_0) {
-        lo0 = (lo0 + 0x78787878u) ^ 0x80808080u; lo1 = (lo1 + 0x78787878u) ^ 0x80808080u;
-        hi0 = (hi0 + 0x78787878u) ^ 0x80808080u; hi1 = (hi1 + 0x78787878u) ^ 0x80808080u;
-    } else if (TYPE == SHS_TYPE_Q5_0) {
-        lo0 = (lo0 + 0x70707070u) ^ 0x80808080u; lo1 = (lo1 + 0x70707070u) ^ 0x80808080u;
-        hi0 = (hi0 + 0x70707070u) ^ 0x80808080u; hi1 = (hi1 + 0x70707070u) ^ 0x80808080u;
-    }
-    v4i r;
-    r[0] = (int)lo0; r[1] = (int)lo1; r[2] = (int)hi0; r[3] = (int)hi1;
-    return r;
-}
-
-template <int TYPE>
-__device__ inline v4i load_weights(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh, int64_t rec,
-                                   int ri, int h)
-{
-    if (TYPE == SHS_TYPE_Q8_0) {
-        return *reinterpret_cast<const v4i*>(wqs + rec * 1024 + ri * 32 + h * 16);
-    } else {
-        uint2 q = *reinterpret_cast<const uint2*>(wqs + rec * 512 + ri * 16 + h * 8);
-        uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
-        return unpack_half<TYPE>(q.x, q.y, qh, h);
-    }
-}
-
-// Operands of one 32-wide quant block for one wave: the 32-row weight tile and TT token tiles.
-template <int TT> struct GemmOps {
-    v4i w;
-    float4 d[4], m[4];
-    v4i x[TT];
-    float da[TT], ds[TT];
-};
-
-template <int TYPE, int TT>
-__device__ __forceinline__ void gemm_load(GemmOps<TT>& o, const uint8_t* __restrict__ wqs,
-                                          const uint32_t* __restrict__ wqh, const float* __restrict__ wd,
-                                          const float* __restrict__ wm, const ActQ8& a, int rt, int B, int b,
-                                          int tt0, int nv, int j, int h)
-{
-    constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
-    const int64_t rec = (int64_t)rt * B + b;
-    o.w = load_weights<TYPE>(wqs, wqh, rec, j, h);
-    const float4* dp = reinterpret_cast<const float4*>(wd + rec * 32);
-#pragma unroll
-    for (int g = 0; g < 4; g++) o.d[g] = dp[2 * g + h];
-    if (OFF) {
-        const float4* mp = reinterpret_cast<const float4*>(wm + rec * 32);
-#pragma unroll
-        for (int g = 0; g < 4; g++) o.m[g] = mp[2 * g + h];
-    }
-#pragma unroll
-    for (int u = 0; u < TT; u++) {
-        if (u < nv) {
-            const int tile = tt0 + u;
-            o.x[u] = *reinterpret_cast<const v4i*>(a.q + ((int64_t)tile * B + b) * 1024 + j * 32 + h * 16);
-            o.da[u] = a.d[(int64_t)b * a.Tpad + tile * 32 + j];
-            if (OFF) o.ds[u] = a.ds[(int64_t)b * a.Tpad + tile * 32 + j];
-        }
-    }
-}
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 __device__ __forceinline__ float f4get(const float4& v, int k)
 {
     return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
 }
 
-// One wave: a 32-row tile × TT 32-token tiles, K consumed one 32-wide quant block per
-// v_mfma_i32_32x32x32_i8. D[i][j] (row i, token j) sits in lane j + 32·(i%8 / 4), register
-// 4·(i/8) + i%4. Each output then takes, block by block in order, exactly the reference's
-// acc = fma(float(I), RN(d_w·d_a), acc) (+ fma(m_w, RN(d_a·Σq), acc) for offset types).
-// The next block's operands are loaded into registers while the current block computes.
+// Four 4-bit fifth-bit flags → 0x10 in the byte of each set bit.
+__device__ inline uint32_t expand_bits4(uint32_t x4)
+{
+    return ((__umul24(x4, 0x00204081u)) & 0x01010101u) << 4;
+}
+
+// Four weight bytes (each < 256, already offset to be unsigned) → two dwords of fp16
+// 1024 + byte, then minus (1024 + zero point): exact small integers.
+__device__ __forceinline__ void bytes_to_half(uint32_t x, _Float16 bias, uint32_t& lo, uint32_t& hi)
+{
+    const h2 b2 = {bias, bias};
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
+    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, p0) + b2);
+    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, p1) + b2);
+}
+
+// Lane half h's MFMA A operands for one 32-wide block of one row: lo = quant elements
+// 8h..8h+7, hi = elements 16+8h..16+8h+7, as fp16 signed weights u − z (u for the
+// offset types). q0/q1 are qs bytes 8h..8h+7 (Q4/Q5) or, for Q8_0, the lane's 16 permuted
+// bytes are q0..q3.
+template <int TYPE>
+__device__ __forceinline__ void weights_to_half(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, uint32_t qh, int h,
+                                                v8h& lo, v8h& hi)
+{
+    uint32_t e0, e1, e2, e3;  // four dwords of unsigned bytes: elements lo[0..3], lo[4..7], hi[0..3], hi[4..7]
+    _Float16 bias;
+    if (TYPE == SHS_TYPE_Q8_0) {
+        e0 = q0 ^ 0x80808080u; e1 = q1 ^ 0x80808080u; e2 = q2 ^ 0x80808080u; e3 = q3 ^ 0x80808080u;
+        bias = (_Float16)-1152.0f;
+    } else {
+        e0 = q0 & 0x0F0F0F0Fu; e1 = q1 & 0x0F0F0F0Fu;
+        e2 = (q0 >> 4) & 0x0F0F0F0Fu; e3 = (q1 >> 4) & 0x0F0F0F0Fu;
+        if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) {
+            const uint32_t sh = 8u * h;
+            e0 |= expand_bits4((qh >> sh) & 0xFu);
+            e1 |= expand_bits4((qh >> (sh + 4)) & 0xFu);
+            e2 |= expand_bits4((qh >> (sh + 16)) & 0xFu);
+            e3 |= expand_bits4((qh >> (sh + 20)) & 0xFu);
+        }
+        bias = TYPE == SHS_TYPE_Q4_0 ? (_Float16)-1032.0f : TYPE == SHS_TYPE_Q5_0 ? (_Float16)-1040.0f : (_Float16)-1024.0f;
+    }
+    uint32_t d[8];
+    bytes_to_half(e0, bias, d[0], d[1]);
+    bytes_to_half(e1, bias, d[2], d[3]);
+    bytes_to_half(e2, bias, d[4], d[5]);
+    bytes_to_half(e3, bias, d[6], d[7]);
+    uint4 l4 = make_uint4(d[0], d[1], d[2], d[3]), h4 = make_uint4(d[4], d[5], d[6], d[7]);
+    lo = __builtin_bit_cast(v8h, l4);
+    hi = __builtin_bit_cast(v8h, h4);
+}
+
+template <int TYPE>
+__device__ __forceinline__ void load_weight_half(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                                                 int64_t rec, int ri, int h, v8h& lo, v8h& hi)
+{
+    if (TYPE == SHS_TYPE_Q8_0) {
+        const uint4 q = *reinterpret_cast<const uint4*>(wqs + rec * 1024 + ri * 32 + h * 16);
+        weights_to_half<TYPE>(q.x, q.y, q.z, q.w, 0u, h, lo, hi);
+    } else {
+        const uint2 q = *reinterpret_cast<const uint2*>(wqs + rec * 512 + ri * 16 + h * 8);
+        const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
+        weights_to_half<TYPE>(q.x, q.y, 0u, 0u, qh, h, lo, hi);
+    }
+}
+
+// The GEMM, by 32-row × 32-token tiles and pairs of quant blocks.
+//  * Integer block sums: two v_mfma_f32_32x32x16_f16 per block on exact fp16 integers
+//    (|w| ≤ 128, |q| ≤ 127, |Σ| < 2^24), so D = float(I_b) exactly.
+//  * Scale tile RN(d_w·d_a) for the two blocks of a pair: one v_mfma_f32_32x32x1_2b_f32
+//    (its block-1 lanes carry the second block), which computes fma(d_w, d_a, 0).
+//  * Epilogue, block by block in order: acc = fma(I_b, S_b, acc) (+ fma(m_w, RN(d_a·Σq),
+//    acc) for the offset types) — IntegerGemm.Multiply4/Multiply1 per output, bit for bit.
+// A block of 4 waves covers 4 row tiles × TT token tiles. The token tiles' activations
+// (fp16, 2 KB per tile and block) are staged in LDS, double-buffered, shared by the waves;
+// each wave streams its own weights. D[i][j] (row i, token j) sits in lane j + 32·(i%8/4),
+// register 4·(i/8) + i%4.
 template <int TYPE, int TT, int MODE>
 __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                               const float* __restrict__ wd, const float* __restrict__ wm,
                                               int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N)
 {
     constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int STAGE = TT * 2 * 128;  // uint4 per pair stage: TT tiles × 2 blocks × 2 KB
+    __shared__ uint4 Bs[2][STAGE];
+    __shared__ float Ds[2][2][TT * 32];
+    __shared__ float DSs[2][2][OFF ? TT * 32 : 1];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
     const int rt = blockIdx.x * 4 + wave;
-    if (rt >= ntiles) return;
+    const bool active = rt < ntiles;
     const int ntt = a.Tpad >> 5;
     const int tt0 = blockIdx.y * TT;
     int nv = ntt - tt0;
     nv = nv < TT ? nv : TT;
+    const int npairs = (B + 1) >> 1;
+    const uint4* aq = reinterpret_cast<const uint4*>(a.q);
+
+    // Stage loader: thread tid owns uint4 slots tid + 256k of the pair's B tile, and
+    // (tid < 2·TT·32) one da / ds value.
+    uint4 st[TT];
+    float sd = 0.0f, sds = 0.0f;
+    auto stage_load = [&](int p) {
+#pragma unroll
+        for (int k = 0; k < TT; k++) {
+            const int e = tid + 256 * k;
+            const int u = e >> 8, rem = e & 255, bb = rem >> 7, off = rem & 127;
+            const int blk = 2 * p + bb;
+            st[k] = make_uint4(0, 0, 0, 0);
+            if (u < nv && blk < B) st[k] = aq[((int64_t)(tt0 + u) * B + blk) * 128 + off];
+        }
+        if (tid < 2 * TT * 32) {
+            const int bb = tid / (TT * 32), tok = tid % (TT * 32);
+            const int blk = 2 * p + bb;
+            const int u = tok >> 5;
+            sd = 0.0f;
+            sds = 0.0f;
+            if (u < nv && blk < B) {
+                sd = a.d[(int64_t)blk * a.Tpad + tt0 * 32 + tok];
+                if (OFF) sds = a.ds[(int64_t)blk * a.Tpad + tt0 * 32 + tok];
+            }
+        }
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < TT; k++) Bs[buf][tid + 256 * k] = st[k];
+        if (tid < 2 * TT * 32) {
+            const int bb = tid / (TT * 32), tok = tid % (TT * 32);
+            Ds[buf][bb][tok] = sd;
+            if (OFF) DSs[buf][bb][tok] = sds;
+        }
+    };
+
+    // Per-wave weight operands of a pair (prefetched one pair ahead).
+    struct W {
+        v8h lo[2], hi[2];
+        float dw;
+        float4 m[2][4];
+    };
+    auto weight_load = [&](int p, W& w) {
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            const int blk = 2 * p + bb;
+            if (active && blk < B) {
+                load_weight_half<TYPE>(wqs, wqh, (int64_t)rt * B + blk, j, h, w.lo[bb], w.hi[bb]);
+                if (OFF) {
+                    const float4* mp = reinterpret_cast<const float4*>(wm + ((int64_t)rt * B + blk) * 32);
+#pragma unroll
+                    for (int g = 0; g < 4; g++) w.m[bb][g] = mp[2 * g + h];
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) { w.lo[bb][e] = (_Float16)0.0f; w.hi[bb][e] = (_Float16)0.0f; }
+                if (OFF)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) w.m[bb][g] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+        const int blk = 2 * p + h;  // the scale MFMA's block-h lanes carry block 2p + h
+        w.dw = (active && blk < B) ? wd[((int64_t)rt * B + blk) * 32 + j] : 0.0f;
+    };
 
     v16f acc[TT];
 #pragma unroll
     for (int u = 0; u < TT; u++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[u][r] = 0.0f;
-    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    v32f zero32;
+#pragma unroll
+    for (int r = 0; r < 32; r++) zero32[r] = 0.0f;
 
-    GemmOps<TT> cur, nxt;
-    gemm_load<TYPE, TT>(cur, wqs, wqh, wd, wm, a, rt, B, 0, tt0, nv, j, h);
-    for (int b = 0; b < B; ++b) {
-        if (b + 1 < B) gemm_load<TYPE, TT>(nxt, wqs, wqh, wd, wm, a, rt, B, b + 1, tt0, nv, j, h);
+    W cur, nxt;
+    stage_load(0);
+    stage_store(0);
+    weight_load(0, cur);
+    __syncthreads();
+    for (int p = 0; p < npairs; ++p) {
+        const int buf = p & 1;
+        const bool more = p + 1 < npairs;
+        if (more) {
+            stage_load(p + 1);
+            weight_load(p + 1, nxt);
+        }
+        if (active) {
 #pragma unroll
-        for (int u = 0; u < TT; u++) {
-            if (u < nv) {
-                const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.w, cur.x[u], zero, 0, 0, 0);
+            for (int u = 0; u < TT; u++) {
+                if (u < nv) {
+                    const float da = Ds[buf][h][u * 32 + j];
+                    const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(cur.dw, da, zero32, 0, 0, 0);
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float sc = f4get(cur.d[r >> 2], r & 3) * cur.da[u];
-                    acc[u][r] = fmaf((float)D[r], sc, acc[u][r]);
-                }
-                if (OFF) {
+                    for (int bb = 0; bb < 2; bb++) {
+                        const uint4* bp = &Bs[buf][(u * 2 + bb) * 128 + j * 4 + 2 * h];
+                        const v8h blo = __builtin_bit_cast(v8h, bp[0]);
+                        const v8h bhi = __builtin_bit_cast(v8h, bp[1]);
+                        v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.lo[bb], blo, zero16, 0, 0, 0);
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.hi[bb], bhi, I, 0, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 16; r++) acc[u][r] = fmaf(f4get(cur.m[r >> 2], r & 3), cur.ds[u], acc[u][r]);
+                        for (int r = 0; r < 16; r++) acc[u][r] = fmaf(I[r], S[16 * bb + r], acc[u][r]);
+                        if (OFF) {
+                            const float dsv = DSs[buf][bb][u * 32 + j];
+#pragma unroll
+                            for (int r = 0; r < 16; r++)
+                                acc[u][r] = fmaf(f4get(cur.m[bb][r >> 2], r & 3), dsv, acc[u][r]);
+                        }
+                    }
                 }
             }
         }
-        cur = nxt;
+        if (more) {
+            stage_store(buf ^ 1);
+            cur = nxt;
+        }
+        __syncthreads();
     }
+    if (!active) return;
 
     const bool vec = ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
 #pragma unroll
@@ -440,13 +533,13 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
         for (int g = 0; g < 4; g++) {
             const int row = rt * 32 + 8 * g + 4 * h;
             if (vec && row + 3 < N) {
-                float4* p = reinterpret_cast<float4*>(yr + row);
+                float4* pp = reinterpret_cast<float4*>(yr + row);
                 float4 v = make_float4(acc[u][4 * g], acc[u][4 * g + 1], acc[u][4 * g + 2], acc[u][4 * g + 3]);
                 if (MODE == GEMM_ADD) {
-                    float4 o = *p;
+                    float4 o = *pp;
                     v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
                 }
-                *p = v;
+                *pp = v;
             } else {
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
@@ -472,13 +565,14 @@ static hipError_t gemm_tt(const DevMatrix& w, const ActQ8& a, float* y, int ldy,
     return hipGetLastError();
 }
 
+// Token tiles per block: the largest of 4/2/1 that still gives ≥ 512 blocks (two per CU).
 template <int TYPE>
 static hipError_t gemm_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
 {
-    int ntt = a.Tpad >> 5;
-    if (ntt <= 1) return gemm_tt<TYPE, 1>(w, a, y, ldy, mode, s);
-    if (ntt <= 2) return gemm_tt<TYPE, 2>(w, a, y, ldy, mode, s);
-    return gemm_tt<TYPE, 4>(w, a, y, ldy, mode, s);
+    const int ntt = a.Tpad >> 5, rg = (w.tiles + 3) / 4;
+    if (ntt >= 4 && rg * ((ntt + 3) / 4) >= 512) return gemm_tt<TYPE, 4>(w, a, y, ldy, mode, s);
+    if (ntt >= 2 && rg * ((ntt + 1) / 2) >= 384) return gemm_tt<TYPE, 2>(w, a, y, ldy, mode, s);
+    return gemm_tt<TYPE, 1>(w, a, y, ldy, mode, s);
 }
 
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
@@ -493,7 +587,7 @@ hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, in
     }
 }
 
-// The raw MFMA int32 block sums, out[t][r][b] — parity instrumentation.
+// The MFMA's exact block sums, out[t][r][b] — parity instrumentation.
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_gemm_sums(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                    int ntiles, int B, ActQ8 a, int32_t* __restrict__ out, int N)
@@ -503,17 +597,19 @@ __global__ __launch_bounds__(256) void k_gemm_sums(const uint8_t* __restrict__ w
     const int rt = blockIdx.x * 4 + wave;
     if (rt >= ntiles) return;
     const int tile = blockIdx.y;
-    const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    const v16f zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const int token = tile * 32 + j;
+    const uint4* aq = reinterpret_cast<const uint4*>(a.q);
     for (int b = 0; b < B; ++b) {
-        const int64_t rec = (int64_t)rt * B + b;
-        const v4i wv = load_weights<TYPE>(wqs, wqh, rec, j, h);
-        const v4i xv = *reinterpret_cast<const v4i*>(a.q + ((int64_t)tile * B + b) * 1024 + j * 32 + h * 16);
-        const v16i D = __builtin_amdgcn_mfma_i32_32x32x32_i8(wv, xv, zero, 0, 0, 0);
+        v8h lo, hi;
+        load_weight_half<TYPE>(wqs, wqh, (int64_t)rt * B + b, j, h, lo, hi);
+        const uint4* bp = aq + ((int64_t)tile * B + b) * 128 + j * 4 + 2 * h;
+        v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(lo, __builtin_bit_cast(v8h, bp[0]), zero16, 0, 0, 0);
+        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(hi, __builtin_bit_cast(v8h, bp[1]), I, 0, 0, 0);
         if (token < a.T)
             for (int r = 0; r < 16; r++) {
                 const int row = rt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < N) out[((int64_t)token * N + row) * B + b] = D[r];
+                if (row < N) out[((int64_t)token * N + row) * B + b] = (int32_t)I[r];
             }
     }
 }
@@ -534,10 +630,20 @@ hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* o
 
 // ------------------------------------------------------ GEMV (selected rows)
 
-// One thread per (token, selected row): the same exact integer block sums (v_dot4_i32_i8
-// on the same byte pairing the MFMA lanes use) and the same serial epilogue, so every
-// value equals the corresponding entry of the full GEMM bit for bit
-// (QuantMatMul.ForwardRowsAsync, QuantMatMul.cs:98-110).
+// Weight element e (0..31) of one row's block as a signed integer (u − z, or u).
+template <int TYPE>
+__device__ __forceinline__ int weight_elem(const uint8_t* q, uint32_t qh, int e)
+{
+    if (TYPE == SHS_TYPE_Q8_0) return (int)(int8_t)q[e];
+    const int j = e & 15;
+    int u = e < 16 ? (q[j] & 0x0F) : (q[j] >> 4);
+    if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) u |= (int)(((qh >> e) & 1u) << 4);
+    return TYPE == SHS_TYPE_Q4_0 ? u - 8 : TYPE == SHS_TYPE_Q5_0 ? u - 16 : u;
+}
+
+// One thread per (token, selected row): the same exact integer block sums and the same
+// serial epilogue as the GEMM, so every value equals the corresponding entry of the
+// full product bit for bit (QuantMatMul.ForwardRowsAsync, QuantMatMul.cs:98-110).
 template <int TYPE>
 __global__ void k_gemv_rows(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                             const float* __restrict__ wd, const float* __restrict__ wm, int B,
@@ -549,31 +655,21 @@ __global__ void k_gemv_rows(const uint8_t* __restrict__ wqs, const uint32_t* __r
     const int i = (int)(idx % n_ids), t = (int)(idx / n_ids);
     const int r = ids[i];
     const int ri = r & 31;
+    const uint16_t* qa = a.q;
     float acc = 0.0f;
     for (int b = 0; b < B; ++b) {
         const int64_t rec = (int64_t)(r >> 5) * B + b;
-        const uint4* ap = reinterpret_cast<const uint4*>(a.q + ((int64_t)(t >> 5) * B + b) * 1024 + (t & 31) * 32);
-        const uint4 a0 = ap[0], a1 = ap[1];
-        v4i w0, w1;
-        if (TYPE == SHS_TYPE_Q8_0) {
-            const v4i* wp = reinterpret_cast<const v4i*>(wqs + rec * 1024 + ri * 32);
-            w0 = wp[0];
-            w1 = wp[1];
-        } else {
-            const uint4 q = *reinterpret_cast<const uint4*>(wqs + rec * 512 + ri * 16);
-            const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
-            w0 = unpack_half<TYPE>(q.x, q.y, qh, 0);
-            w1 = unpack_half<TYPE>(q.z, q.w, qh, 1);
-        }
+        const uint16_t* act = qa + (((int64_t)(t >> 5) * B + b) * 32 + (t & 31)) * 32;
         int I = 0;
-        I = __builtin_amdgcn_sdot4(w0[0], (int)a0.x, I, false);
-        I = __builtin_amdgcn_sdot4(w0[1], (int)a0.y, I, false);
-        I = __builtin_amdgcn_sdot4(w0[2], (int)a0.z, I, false);
-        I = __builtin_amdgcn_sdot4(w0[3], (int)a0.w, I, false);
-        I = __builtin_amdgcn_sdot4(w1[0], (int)a1.x, I, false);
-        I = __builtin_amdgcn_sdot4(w1[1], (int)a1.y, I, false);
-        I = __builtin_amdgcn_sdot4(w1[2], (int)a1.z, I, false);
-        I = __builtin_amdgcn_sdot4(w1[3], (int)a1.w, I, false);
+        if (TYPE == SHS_TYPE_Q8_0) {
+            const uint8_t* q = wqs + rec * 1024 + ri * 32;  // stored in the activation order
+            for (int p = 0; p < 32; p++) I += (int)(int8_t)q[p] * (int)__builtin_bit_cast(_Float16, act[p]);
+        } else {
+            const uint8_t* q = wqs + rec * 512 + ri * 16;
+            const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
+            for (int p = 0; p < 32; p++)
+                I += weight_elem<TYPE>(q, qh, perm_elem(p)) * (int)__builtin_bit_cast(_Float16, act[p]);
+        }
         const float da = a.d[(int64_t)b * a.Tpad + t];
         const float sc = wd[rec * 32 + ri] * da;
         acc = fmaf((float)I, sc, acc);
