@@ -104,7 +104,10 @@ void free_matrix(DevMatrix& m)
     m = DevMatrix();
 }
 
-hipError_t alloc_matrix(DevMatrix& m, int type, int rows, int cols)
+// Allocates a repacked matrix and clears it on stream s, the stream its rows are then
+// uploaded on: a clear on another stream (hipMemset runs on the null stream, which a
+// non-blocking stream does not wait for) could land after the repack and erase it.
+hipError_t alloc_matrix(DevMatrix& m, int type, int rows, int cols, hipStream_t s)
 {
     m.type = type;
     m.rows = rows;
@@ -114,16 +117,16 @@ hipError_t alloc_matrix(DevMatrix& m, int type, int rows, int cols)
     size_t recs = (size_t)m.tiles * m.blocks;
     hipError_t e;
     if ((e = hipMalloc((void**)&m.qs, recs * 32 * qs_bytes(type))) != hipSuccess) return e;
-    if ((e = hipMemset(m.qs, 0, recs * 32 * qs_bytes(type))) != hipSuccess) return e;
+    if ((e = hipMemsetAsync(m.qs, 0, recs * 32 * qs_bytes(type), s)) != hipSuccess) return e;
     if ((e = hipMalloc((void**)&m.d, recs * 32 * sizeof(float))) != hipSuccess) return e;
-    if ((e = hipMemset(m.d, 0, recs * 32 * sizeof(float))) != hipSuccess) return e;
+    if ((e = hipMemsetAsync(m.d, 0, recs * 32 * sizeof(float), s)) != hipSuccess) return e;
     if (type_has_qh(type)) {
         if ((e = hipMalloc((void**)&m.qh, recs * 32 * sizeof(uint32_t))) != hipSuccess) return e;
-        if ((e = hipMemset(m.qh, 0, recs * 32 * sizeof(uint32_t))) != hipSuccess) return e;
+        if ((e = hipMemsetAsync(m.qh, 0, recs * 32 * sizeof(uint32_t), s)) != hipSuccess) return e;
     }
     if (type_has_offset(type)) {
         if ((e = hipMalloc((void**)&m.m, recs * 32 * sizeof(float))) != hipSuccess) return e;
-        if ((e = hipMemset(m.m, 0, recs * 32 * sizeof(float))) != hipSuccess) return e;
+        if ((e = hipMemsetAsync(m.m, 0, recs * 32 * sizeof(float), s)) != hipSuccess) return e;
     }
     return hipSuccess;
 }
@@ -404,9 +407,12 @@ static shs_status ensure_rope(shs_model* m, int need)
     HIP_TRY(m->cos_tab.ensure(c.size() * sizeof(float)));
     HIP_TRY(m->sin_tab.ensure(s.size() * sizeof(float)));
     HIP_TRY(m->qscale_tab.ensure(qs.size() * sizeof(float)));
-    HIP_TRY(hipMemcpy(m->cos_tab.p, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(m->sin_tab.p, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice));
-    HIP_TRY(hipMemcpy(m->qscale_tab.p, qs.data(), qs.size() * sizeof(float), hipMemcpyHostToDevice));
+    // Copied on the model's stream (which the kernels that read the tables run on) and
+    // waited for before the host vectors go out of scope.
+    HIP_TRY(hipMemcpyAsync(m->cos_tab.p, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->sin_tab.p, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipMemcpyAsync(m->qscale_tab.p, qs.data(), qs.size() * sizeof(float), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
     m->rope_cap = cap;
     return SHS_OK;
 }
@@ -501,7 +507,7 @@ shs_status load_proj(shs_model* m, Proj& p, const std::vector<const Spec*>& ts, 
     p.parts.reserve(ts.size());
     if (same && aligned) {
         DevMatrix w;
-        HIP_TRY(alloc_matrix(w, ts[0]->type, total, (int)ts[0]->ne0));
+        HIP_TRY(alloc_matrix(w, ts[0]->type, total, (int)ts[0]->ne0, m->stream));
         p.parts.push_back(w);
         p.col0.push_back(0);
         int row0 = 0;
@@ -518,7 +524,7 @@ shs_status load_proj(shs_model* m, Proj& p, const std::vector<const Spec*>& ts, 
         int c0 = 0;
         for (auto* t : ts) {
             DevMatrix w;
-            HIP_TRY(alloc_matrix(w, t->type, (int)t->ne1, (int)t->ne0));
+            HIP_TRY(alloc_matrix(w, t->type, (int)t->ne1, (int)t->ne0, m->stream));
             p.parts.push_back(w);
             HIP_TRY(upload_rows(p.parts.back(), t->src, 0, (int)t->ne1, staging, m->stream));
             p.col0.push_back(c0);
@@ -553,7 +559,8 @@ shs_status upload_vector(shs_model* m, const Spec* t, int64_t n, float** out)
         } else {
             return fail(SHS_E_NOT_SUPPORTED, "norm tensor '%s' is %s; F32 or F16 expected", t->name.c_str(), type_name(t->type));
         }
-        HIP_TRY(hipMemcpy(*out, v.data(), n * sizeof(float), hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpyAsync(*out, v.data(), n * sizeof(float), hipMemcpyHostToDevice, m->stream));
+        HIP_TRY(hipStreamSynchronize(m->stream));
     }
     m->where[t->name] = TensorLoc{nullptr, 0, 0, *out, (int)n};
     return SHS_OK;
@@ -618,7 +625,7 @@ shs_status build_model(const shs_config& c, const SpecMap& tm, int device, int i
     const Spec* t;
     if ((st = need_tensor(tm, "token_embd.weight", &t)) != SHS_OK) return bail(st);
     if ((st = check_matrix(t, c.hidden, c.vocab)) != SHS_OK) return bail(st);
-    if ((e = alloc_matrix(m->embd, t->type, c.vocab, c.hidden)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(token_embd)"));
+    if ((e = alloc_matrix(m->embd, t->type, c.vocab, c.hidden, m->stream)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(token_embd)"));
     if ((e = upload_rows(m->embd, t->src, 0, c.vocab, staging, m->stream)) != hipSuccess) return bail(hip_fail(e, "upload token_embd"));
     m->where[t->name] = TensorLoc{&m->embd, 0, c.vocab, nullptr, 0};
     // Shieldstral ties the LM head to token_embd; output.weight is used when present
@@ -626,7 +633,7 @@ shs_status build_model(const shs_config& c, const SpecMap& tm, int device, int i
     const Spec* head = tm.get("output.weight");
     if (head) {
         if ((st = check_matrix(head, c.hidden, c.vocab)) != SHS_OK) return bail(st);
-        if ((e = alloc_matrix(m->head, head->type, c.vocab, c.hidden)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(output)"));
+        if ((e = alloc_matrix(m->head, head->type, c.vocab, c.hidden, m->stream)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(output)"));
         if ((e = upload_rows(m->head, head->src, 0, c.vocab, staging, m->stream)) != hipSuccess) return bail(hip_fail(e, "upload output"));
         m->tied = false;
         m->where[head->name] = TensorLoc{&m->head, 0, c.vocab, nullptr, 0};
@@ -1270,7 +1277,7 @@ extern "C" shs_status shs_matrix_create(int32_t type, int32_t rows, int32_t cols
     shs_matrix* m = new shs_matrix();
     m->device = device;
     hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
-    if (e == hipSuccess) e = alloc_matrix(m->w, type, rows, cols);
+    if (e == hipSuccess) e = alloc_matrix(m->w, type, rows, cols, m->stream);
     Buf staging;
     if (e == hipSuccess) e = upload_rows(m->w, host_src(data), 0, rows, staging, m->stream);
     if (e != hipSuccess) {

@@ -370,6 +370,13 @@ __device__ __forceinline__ void load_weight_half(const uint8_t* __restrict__ wqs
     }
 }
 
+// Chunk swizzle of a 64-byte token row in LDS: rows j..j+7 (and j..j+15) map chunk c to
+// distinct 16-byte bank groups.
+__device__ __forceinline__ int row_swz(int row)
+{
+    return ((row >> 1) ^ (row >> 3)) & 3;
+}
+
 // The GEMM, by 32-row × 32-token tiles and pairs of quant blocks.
 //  * Integer block sums: two v_mfma_f32_32x32x16_f16 per block on exact fp16 integers
 //    (|w| ≤ 128, |q| ≤ 127, |Σ| < 2^24), so D = float(I_b) exactly.
@@ -395,6 +402,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
+    const int jswz = row_swz(j);
     const int rt = blockIdx.x * 4 + wave;
     const bool active = rt < ntiles;
     const int ntt = a.Tpad >> 5;
@@ -429,9 +437,12 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
             }
         }
     };
+    // LDS holds each token row's four 16-byte chunks XOR-swizzled by the row (row_swz), so
+    // the 32 rows one ds_read_b128 touches fall in distinct banks.
+    const int st_slot = (tid & ~3) | ((tid & 3) ^ row_swz((tid & 127) >> 2));
     auto stage_store = [&](int buf) {
 #pragma unroll
-        for (int k = 0; k < TT; k++) Bs[buf][tid + 256 * k] = st[k];
+        for (int k = 0; k < TT; k++) Bs[buf][st_slot + 256 * k] = st[k];
         if (tid < 2 * TT * 32) {
             const int bb = tid / (TT * 32), tok = tid % (TT * 32);
             Ds[buf][bb][tok] = sd;
@@ -498,9 +509,9 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
                     const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(cur.dw, da, zero32, 0, 0, 0);
 #pragma unroll
                     for (int bb = 0; bb < 2; bb++) {
-                        const uint4* bp = &Bs[buf][(u * 2 + bb) * 128 + j * 4 + 2 * h];
-                        const v8h blo = __builtin_bit_cast(v8h, bp[0]);
-                        const v8h bhi = __builtin_bit_cast(v8h, bp[1]);
+                        const uint4* bp = &Bs[buf][(u * 2 + bb) * 128 + j * 4];
+                        const v8h blo = __builtin_bit_cast(v8h, bp[(2 * h) ^ jswz]);
+                        const v8h bhi = __builtin_bit_cast(v8h, bp[(2 * h + 1) ^ jswz]);
                         v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.lo[bb], blo, zero16, 0, 0, 0);
                         I = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.hi[bb], bhi, I, 0, 0, 0);
 #pragma unroll
