@@ -23,6 +23,40 @@ METRIC = "prefill tok/s + ms/verdict (1k-token prompt), Shieldstral-3B Q4_0, 1 M
 T_PROMPT = 1024
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0
+# The roofline kernel: the fused gate|up projection (18432 x 3072, Q4_0), the largest GEMM
+# of a layer and the only launch of its kernel instantiation.
+ROOF_CLASS = "gemm_gate_up"
+ROOF_KERNEL = "k_gemm<Q4_0, TT=4, STORE>: fused gate|up 18432x3072 Q4_0 weights x 1024 Q8 tokens"
+# HBM bytes per launch of that kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE passes,
+# calibrated against a device copy of known size (written by the profiling procedure).
+TRAFFIC_FILE = ROOT / "profiles" / "k_gemm_gate_up_q4_0_t1024_traffic.md"
+COPY_PROBE_BYTES = 256 << 20
+
+
+def read_traffic():
+    try:
+        for line in TRAFFIC_FILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def copy_probe():
+    """One device-to-device copy of COPY_PROBE_BYTES through the HIP runtime the library uses:
+    the known-size reference dispatch that scales the FETCH_SIZE / WRITE_SIZE counters."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so.7")
+    a, b = C.c_void_p(), C.c_void_p()
+    assert hip.hipMalloc(C.byref(a), C.c_size_t(COPY_PROBE_BYTES)) == 0
+    assert hip.hipMalloc(C.byref(b), C.c_size_t(COPY_PROBE_BYTES)) == 0
+    assert hip.hipMemset(a, 1, C.c_size_t(COPY_PROBE_BYTES)) == 0
+    assert hip.hipDeviceSynchronize() == 0
+    assert hip.hipMemcpy(b, a, C.c_size_t(COPY_PROBE_BYTES), 3) == 0  # hipMemcpyDeviceToDevice
+    assert hip.hipDeviceSynchronize() == 0
+    hip.hipFree(a)
+    hip.hipFree(b)
 
 
 def gemm_flops_per_layer(cfg, T):
@@ -68,6 +102,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=T_PROMPT)
     ap.add_argument("--seed", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help=f"first copy {COPY_PROBE_BYTES >> 20} MiB device to device (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the verdict path does not shard "
@@ -79,6 +115,9 @@ def main():
 
     cfg = S.SHIELDSTRAL_3B
     T = args.tokens
+    S.load_library()
+    if args.copy_probe:
+        copy_probe()
     model = S.MinistralModel.synthetic(cfg, S.Q4_0, seed=args.seed, initial_cache_capacity=T)
     rng = np.random.default_rng(args.seed)
     tokens = rng.integers(0, cfg.vocab_size, T).astype(np.int32)
@@ -106,13 +145,17 @@ def main():
     model.profile(False)
     ms = elapsed / args.steps * 1e3
 
-    n, gemm_ms, gemm_ops = model.profile_read("gemm")
-    achieved = gemm_ops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
+    n, roof_ms, roof_ops = model.profile_read(ROOF_CLASS)
+    achieved = roof_ops / (roof_ms * 1e-3) / 1e12 if roof_ms > 0 else 0.0
     breakdown = {}
-    for cls in ("gemm", "attention", "rmsnorm_quant", "swiglu_quant", "quant_act", "rope_store", "embed", "gemv"):
-        c, cms, _ = model.profile_read(cls)
+    for cls in ("gemm*", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "attention", "rmsnorm_quant",
+                "swiglu_quant", "quant_act", "rope_store", "embed", "gemv"):
+        c, cms, cops = model.profile_read(cls)
         if c:
-            breakdown[cls] = {"launches_per_step": c // args.steps, "ms_per_step": round(cms / args.steps, 4)}
+            e = {"launches_per_step": c // args.steps, "ms_per_step": round(cms / args.steps, 4)}
+            if cops:
+                e["tops"] = round(cops / (cms * 1e-3) / 1e12, 1)
+            breakdown[cls.rstrip("*") + ("_all" if cls.endswith("*") else "")] = e
 
     line = {
         "metric": METRIC,
@@ -133,11 +176,11 @@ def main():
                    "layers": cfg.layer_count, "hidden": cfg.hidden_size, "ffn": cfg.feed_forward_size,
                    "heads": cfg.head_count, "kv_heads": cfg.kv_head_count, "vocab": cfg.vocab_size,
                    "tokens": T, "weights": "Q4_0", "seed": args.seed},
-        "roofline": {"bound": "mfma", "kernel": "k_gemm (int8 MFMA, all projections)",
+        "roofline": {"bound": "mfma", "kernel": ROOF_KERNEL,
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": None,
-                     "launches": n, "ms_per_launch": round(gemm_ms / max(n, 1), 5),
-                     "ops_per_launch": round(gemm_ops / max(n, 1))},
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": read_traffic(),
+                     "launches": n, "ms_per_launch": round(roof_ms / max(n, 1), 5),
+                     "ops_per_launch": round(roof_ops / max(n, 1))},
         "breakdown": breakdown,
         "score": result.score,
     }

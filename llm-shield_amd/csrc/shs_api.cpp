@@ -860,10 +860,10 @@ struct Capture {
 
 double gemm_ops(int T, const DevMatrix& w) { return 2.0 * T * (double)w.rows * w.cols; }
 
-shs_status run_proj(shs_model* m, const Proj& p, const ActQ8& a, float* y, int ldy, int mode)
+shs_status run_proj(shs_model* m, const Proj& p, const ActQ8& a, float* y, int ldy, int mode, const char* cls)
 {
     for (size_t i = 0; i < p.parts.size(); i++) {
-        Timed tm(m->prof, "gemm", gemm_ops(a.T, p.parts[i]), m->stream);
+        Timed tm(m->prof, cls, gemm_ops(a.T, p.parts[i]), m->stream);
         HIP_TRY(launch_gemm(p.parts[i], a, y + p.col0[i], ldy, mode, m->stream));
     }
     return SHS_OK;
@@ -926,7 +926,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         snprintf(name, sizeof name, "blk.%d.attn_norm", l);
         if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
 
-        if (run_proj(m, L.qkv, ah, qkv, ldqkv, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+        if (run_proj(m, L.qkv, ah, qkv, ldqkv, GEMM_STORE, "gemm_qkv") != SHS_OK) return SHS_E_DEVICE;
         {
             Timed tm(m->prof, "rope_store", 0, m->stream);
             HIP_TRY(launch_rope_store(qkv, ldqkv, T, c.n_head, c.n_kv_head, c.head_dim, m->pos.as<int32_t>(),
@@ -957,14 +957,14 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             HIP_TRY(launch_quant_act(ctx, qdim, ac, 0, m->stream));
         }
         if (cap_on) {
-            if (run_proj(m, L.o, ac, tmp, hidden, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+            if (run_proj(m, L.o, ac, tmp, hidden, GEMM_STORE, "gemm_o") != SHS_OK) return SHS_E_DEVICE;
             snprintf(name, sizeof name, "blk.%d.attn_out", l);
             if (cp.observe(name, tmp, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
             HIP_TRY(launch_add_inplace(h, tmp, (size_t)T * hidden, m->stream));
             snprintf(name, sizeof name, "blk.%d.post_attn", l);
             if (cp.observe(name, h, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
         } else {
-            if (run_proj(m, L.o, ac, h, hidden, GEMM_ADD) != SHS_OK) return SHS_E_DEVICE;
+            if (run_proj(m, L.o, ac, h, hidden, GEMM_ADD, "gemm_o") != SHS_OK) return SHS_E_DEVICE;
         }
 
         {
@@ -974,7 +974,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         snprintf(name, sizeof name, "blk.%d.ffn_norm", l);
         if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
 
-        if (run_proj(m, L.gu, ah, gu, 2 * c.ffn, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+        if (run_proj(m, L.gu, ah, gu, 2 * c.ffn, GEMM_STORE, "gemm_gate_up") != SHS_OK) return SHS_E_DEVICE;
         ActQ8 af = a;
         af.K = c.ffn;
         af.B = c.ffn / 32;
@@ -983,14 +983,14 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             HIP_TRY(launch_swiglu_quant(gu, 2 * c.ffn, c.ffn, af, nullptr, m->stream));
         }
         if (cap_on) {
-            if (run_proj(m, L.down, af, tmp, hidden, GEMM_STORE) != SHS_OK) return SHS_E_DEVICE;
+            if (run_proj(m, L.down, af, tmp, hidden, GEMM_STORE, "gemm_down") != SHS_OK) return SHS_E_DEVICE;
             snprintf(name, sizeof name, "blk.%d.ffn_out", l);
             if (cp.observe(name, tmp, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
             HIP_TRY(launch_add_inplace(h, tmp, (size_t)T * hidden, m->stream));
             snprintf(name, sizeof name, "blk.%d.output", l);
             if (cp.observe(name, h, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
         } else {
-            if (run_proj(m, L.down, af, h, hidden, GEMM_ADD) != SHS_OK) return SHS_E_DEVICE;
+            if (run_proj(m, L.down, af, h, hidden, GEMM_ADD, "gemm_down") != SHS_OK) return SHS_E_DEVICE;
         }
     }
     return SHS_OK;
@@ -1237,13 +1237,17 @@ extern "C" shs_status shs_profile_read(shs_model* m, const char* cls, int64_t* l
     if (!m || !cls) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
     (void)hipSetDevice(m->device);
     m->prof.collect();
-    auto it = m->prof.totals.find(cls);
+    // "name" reads one class; "prefix*" sums every class that starts with prefix.
+    std::string key(cls);
+    const bool prefix = !key.empty() && key.back() == '*';
+    if (prefix) key.pop_back();
     int64_t n = 0;
     double ms = 0, ops = 0;
-    if (it != m->prof.totals.end()) {
-        n = it->second.first;
-        ms = it->second.second.first;
-        ops = it->second.second.second;
+    for (const auto& kv : m->prof.totals) {
+        if (prefix ? kv.first.compare(0, key.size(), key) != 0 : kv.first != key) continue;
+        n += kv.second.first;
+        ms += kv.second.second.first;
+        ops += kv.second.second.second;
     }
     if (launches) *launches = n;
     if (total_ms) *total_ms = ms;

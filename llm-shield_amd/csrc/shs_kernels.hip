@@ -299,11 +299,6 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float v32f __attribute__((ext_vector_type(32)));
 
-__device__ __forceinline__ float f4get(const float4& v, int k)
-{
-    return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
-}
-
 // Four 4-bit fifth-bit flags → 0x10 in the byte of each set bit.
 __device__ inline uint32_t expand_bits4(uint32_t x4)
 {
@@ -388,16 +383,24 @@ __device__ __forceinline__ int row_swz(int row)
 // (fp16, 2 KB per tile and block) are staged in LDS, double-buffered, shared by the waves;
 // each wave streams its own weights. D[i][j] (row i, token j) sits in lane j + 32·(i%8/4),
 // register 4·(i/8) + i%4.
+// Software pipeline, one barrier per pair: the global loads of pair p+1 (activations, raw
+// weight bytes, scales, mins) are issued before pair p's MFMAs and consumed after them —
+// staged into LDS and decoded into the fp16 operand registers — so their latency hides
+// behind pair p's arithmetic.
 template <int TYPE, int TT, int MODE>
-__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
-                                              const float* __restrict__ wd, const float* __restrict__ wm,
-                                              int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N)
+__global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                                                 const float* __restrict__ wd, const float* __restrict__ wm,
+                                                 int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N)
 {
     constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
+    constexpr bool QH = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1);
+    constexpr bool Q8 = (TYPE == SHS_TYPE_Q8_0);
+    constexpr int QW = Q8 ? 4 : 2;       // raw weight dwords per lane and block
     constexpr int STAGE = TT * 2 * 128;  // uint4 per pair stage: TT tiles × 2 blocks × 2 KB
     __shared__ uint4 Bs[2][STAGE];
     __shared__ float Ds[2][2][TT * 32];
     __shared__ float DSs[2][2][OFF ? TT * 32 : 1];
+    __shared__ float4 Ms[2][4][OFF ? 16 : 1];  // per wave: m of its 32 rows × 2 blocks
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -412,11 +415,15 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
     const int npairs = (B + 1) >> 1;
     const uint4* aq = reinterpret_cast<const uint4*>(a.q);
 
-    // Stage loader: thread tid owns uint4 slots tid + 256k of the pair's B tile, and
-    // (tid < 2·TT·32) one da / ds value.
-    uint4 st[TT];
+    // ---- raw prefetch registers for one pair
+    uint4 st[TT];             // activation chunks: thread tid owns slots tid + 256k
     float sd = 0.0f, sds = 0.0f;
-    auto stage_load = [&](int p) {
+    uint32_t rq[2][QW];       // weight bytes of (row j, lane half h) for blocks 2p, 2p+1
+    uint32_t rqh[2];          // fifth bits of row j, blocks 2p, 2p+1
+    float rdw = 0.0f;         // d_w of (row j, block 2p+h): the scale MFMA's operand
+    float rm = 0.0f;          // m_w of (row j, block 2p+h)
+
+    auto load_raw = [&](int p) {
 #pragma unroll
         for (int k = 0; k < TT; k++) {
             const int e = tid + 256 * k;
@@ -428,19 +435,49 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
         if (tid < 2 * TT * 32) {
             const int bb = tid / (TT * 32), tok = tid % (TT * 32);
             const int blk = 2 * p + bb;
-            const int u = tok >> 5;
             sd = 0.0f;
             sds = 0.0f;
-            if (u < nv && blk < B) {
+            if ((tok >> 5) < nv && blk < B) {
                 sd = a.d[(int64_t)blk * a.Tpad + tt0 * 32 + tok];
                 if (OFF) sds = a.ds[(int64_t)blk * a.Tpad + tt0 * 32 + tok];
             }
         }
+#pragma unroll
+        for (int bb = 0; bb < 2; bb++) {
+            const int blk = 2 * p + bb;
+#pragma unroll
+            for (int w = 0; w < QW; w++) rq[bb][w] = 0u;
+            rqh[bb] = 0u;
+            if (active && blk < B) {
+                const int64_t rec = (int64_t)rt * B + blk;
+                if constexpr (Q8) {
+                    const uint4 q = *reinterpret_cast<const uint4*>(wqs + rec * 1024 + j * 32 + h * 16);
+                    rq[bb][0] = q.x;
+                    rq[bb][1] = q.y;
+                    rq[bb][2] = q.z;
+                    rq[bb][3] = q.w;
+                } else {
+                    const uint2 q = *reinterpret_cast<const uint2*>(wqs + rec * 512 + j * 16 + h * 8);
+                    rq[bb][0] = q.x;
+                    rq[bb][1] = q.y;
+                }
+                if (QH) rqh[bb] = wqh[rec * 32 + j];
+            }
+        }
+        const int blk = 2 * p + h;
+        rdw = 0.0f;
+        rm = 0.0f;
+        if (active && blk < B) {
+            rdw = wd[((int64_t)rt * B + blk) * 32 + j];
+            if (OFF) rm = wm[((int64_t)rt * B + blk) * 32 + j];
+        }
     };
-    // LDS holds each token row's four 16-byte chunks XOR-swizzled by the row (row_swz), so
-    // the 32 rows one ds_read_b128 touches fall in distinct banks.
+
+    // ---- operands of the pair being multiplied
+    v8h wlo[2], whi[2];
+    float dw = 0.0f;
     const int st_slot = (tid & ~3) | ((tid & 3) ^ row_swz((tid & 127) >> 2));
-    auto stage_store = [&](int buf) {
+    auto commit = [&](int buf) {
 #pragma unroll
         for (int k = 0; k < TT; k++) Bs[buf][st_slot + 256 * k] = st[k];
         if (tid < 2 * TT * 32) {
@@ -448,35 +485,15 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
             Ds[buf][bb][tok] = sd;
             if (OFF) DSs[buf][bb][tok] = sds;
         }
-    };
-
-    // Per-wave weight operands of a pair (prefetched one pair ahead).
-    struct W {
-        v8h lo[2], hi[2];
-        float dw;
-        float4 m[2][4];
-    };
-    auto weight_load = [&](int p, W& w) {
+        if (OFF) reinterpret_cast<float*>(Ms[buf][wave])[h * 32 + j] = rm;
 #pragma unroll
         for (int bb = 0; bb < 2; bb++) {
-            const int blk = 2 * p + bb;
-            if (active && blk < B) {
-                load_weight_half<TYPE>(wqs, wqh, (int64_t)rt * B + blk, j, h, w.lo[bb], w.hi[bb]);
-                if (OFF) {
-                    const float4* mp = reinterpret_cast<const float4*>(wm + ((int64_t)rt * B + blk) * 32);
-#pragma unroll
-                    for (int g = 0; g < 4; g++) w.m[bb][g] = mp[2 * g + h];
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) { w.lo[bb][e] = (_Float16)0.0f; w.hi[bb][e] = (_Float16)0.0f; }
-                if (OFF)
-#pragma unroll
-                    for (int g = 0; g < 4; g++) w.m[bb][g] = make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            if constexpr (Q8)
+                weights_to_half<TYPE>(rq[bb][0], rq[bb][1], rq[bb][2], rq[bb][3], 0u, h, wlo[bb], whi[bb]);
+            else
+                weights_to_half<TYPE>(rq[bb][0], rq[bb][1], 0u, 0u, rqh[bb], h, wlo[bb], whi[bb]);
         }
-        const int blk = 2 * p + h;  // the scale MFMA's block-h lanes carry block 2p + h
-        w.dw = (active && blk < B) ? wd[((int64_t)rt * B + blk) * 32 + j] : 0.0f;
+        dw = rdw;
     };
 
     v16f acc[TT];
@@ -489,47 +506,44 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ wqs, c
 #pragma unroll
     for (int r = 0; r < 32; r++) zero32[r] = 0.0f;
 
-    W cur, nxt;
-    stage_load(0);
-    stage_store(0);
-    weight_load(0, cur);
+    load_raw(0);
+    commit(0);
     __syncthreads();
     for (int p = 0; p < npairs; ++p) {
         const int buf = p & 1;
         const bool more = p + 1 < npairs;
-        if (more) {
-            stage_load(p + 1);
-            weight_load(p + 1, nxt);
-        }
+        if (more) load_raw(p + 1);
         if (active) {
 #pragma unroll
             for (int u = 0; u < TT; u++) {
                 if (u < nv) {
                     const float da = Ds[buf][h][u * 32 + j];
-                    const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(cur.dw, da, zero32, 0, 0, 0);
+                    const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
 #pragma unroll
                     for (int bb = 0; bb < 2; bb++) {
                         const uint4* bp = &Bs[buf][(u * 2 + bb) * 128 + j * 4];
                         const v8h blo = __builtin_bit_cast(v8h, bp[(2 * h) ^ jswz]);
                         const v8h bhi = __builtin_bit_cast(v8h, bp[(2 * h + 1) ^ jswz]);
-                        v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.lo[bb], blo, zero16, 0, 0, 0);
-                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(cur.hi[bb], bhi, I, 0, 0, 0);
+                        v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(wlo[bb], blo, zero16, 0, 0, 0);
+                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(whi[bb], bhi, I, 0, 0, 0);
 #pragma unroll
                         for (int r = 0; r < 16; r++) acc[u][r] = fmaf(I[r], S[16 * bb + r], acc[u][r]);
                         if (OFF) {
                             const float dsv = DSs[buf][bb][u * 32 + j];
 #pragma unroll
-                            for (int r = 0; r < 16; r++)
-                                acc[u][r] = fmaf(f4get(cur.m[bb][r >> 2], r & 3), dsv, acc[u][r]);
+                            for (int g = 0; g < 4; g++) {
+                                const float4 m4 = Ms[buf][wave][bb * 8 + 2 * g + h];
+                                acc[u][4 * g] = fmaf(m4.x, dsv, acc[u][4 * g]);
+                                acc[u][4 * g + 1] = fmaf(m4.y, dsv, acc[u][4 * g + 1]);
+                                acc[u][4 * g + 2] = fmaf(m4.z, dsv, acc[u][4 * g + 2]);
+                                acc[u][4 * g + 3] = fmaf(m4.w, dsv, acc[u][4 * g + 3]);
+                            }
                         }
                     }
                 }
             }
         }
-        if (more) {
-            stage_store(buf ^ 1);
-            cur = nxt;
-        }
+        if (more) commit(buf ^ 1);
         __syncthreads();
     }
     if (!active) return;
