@@ -106,82 +106,90 @@ hipError_t launch_repack(const DevMatrix& w, const uint8_t* native, int row0, in
 
 // ---------------------------------------------------- activation quantization
 
-// One 32-value block: IntegerGemm.QuantizeActivations (semantics 0) or
-// IntegerDot.QuantizeActivations (semantics 1). d = max/127 and 1/d are IEEE
-// (correctly rounded division is on for this file).
-__device__ inline void quant32(const float* v, int semantics, int8_t* q, float& dd, float& ds)
+// One 32-value block: IntegerGemm.QuantizeActivations (semantics 0: d = max|x|/127,
+// q = RNE(x·(1/d)), IntegerGemm.cs:97-138) or IntegerDot.QuantizeActivations (1: q rounded
+// half away from zero and clamped to ±127, d rounded to fp16, IntegerDot.cs:60-98); d and
+// 1/d are IEEE (correctly rounded division is on for this file), d = 0 gives q = 0. Also
+// d·Σq, the offset types' second epilogue factor. The 8 lanes of an aligned lane group
+// (l8 = lane % 8) hold elements 4·l8 .. 4·l8+3; max and Σq are exact in any order, so the
+// group reductions are order-free. Each lane stores its 4 fp16 codes at their permuted
+// positions (8 bytes; the group writes the block's 64-byte row).
+__device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, int t, int b, int semantics)
 {
-    float mx = 0.0f;
-    for (int k = 0; k < 32; k++) mx = fmaxf(mx, fabsf(v[k]));
-    float d = mx / 127.0f;
-    float inv = d != 0.0f ? 1.0f / d : 0.0f;
-    int sum = 0;
+    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 4, 8));
+    const float d = mx / 127.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    int q0, q1, q2, q3;
+    float dd;
     if (semantics == 0) {
-        for (int k = 0; k < 32; k++) {
-            int qi = (int)__builtin_rintf(v[k] * inv);
-            q[k] = (int8_t)qi;
-            sum += qi;
-        }
+        q0 = (int)__builtin_rintf(v.x * inv);
+        q1 = (int)__builtin_rintf(v.y * inv);
+        q2 = (int)__builtin_rintf(v.z * inv);
+        q3 = (int)__builtin_rintf(v.w * inv);
         dd = d;
     } else {
-        for (int k = 0; k < 32; k++) {
-            int qi = (int)roundf(v[k] * inv);
-            qi = qi < -127 ? -127 : (qi > 127 ? 127 : qi);
-            q[k] = (int8_t)qi;
-            sum += qi;
-        }
+        q0 = min(127, max(-127, (int)roundf(v.x * inv)));
+        q1 = min(127, max(-127, (int)roundf(v.y * inv)));
+        q2 = min(127, max(-127, (int)roundf(v.z * inv)));
+        q3 = min(127, max(-127, (int)roundf(v.w * inv)));
         dd = round_to_half(d);
     }
-    ds = dd * (float)sum;
-}
-
-__device__ inline void store_q8_block(const ActQ8& a, int t, int b, const int8_t* q, float dd, float ds)
-{
-    uint32_t w[16];
-    for (int p2 = 0; p2 < 16; p2++) {
-        const _Float16 x0 = (_Float16)(float)q[perm_elem(2 * p2)];
-        const _Float16 x1 = (_Float16)(float)q[perm_elem(2 * p2 + 1)];
-        w[p2] = (uint32_t)__builtin_bit_cast(uint16_t, x0) | ((uint32_t)__builtin_bit_cast(uint16_t, x1) << 16);
+    int sum = (q0 + q1) + (q2 + q3);
+    sum += __shfl_xor(sum, 1, 8);
+    sum += __shfl_xor(sum, 2, 8);
+    sum += __shfl_xor(sum, 4, 8);
+    const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q0) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q1) << 16);
+    const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q2) |
+                        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q3) << 16);
+    // element 4·l8 sits at stored position perm⁻¹: groups of 8 keep their order, [8..15] and
+    // [16..23] swap places.
+    const int pos = (l8 == 2 || l8 == 3) ? 4 * l8 + 8 : (l8 == 4 || l8 == 5) ? 4 * l8 - 8 : 4 * l8;
+    uint16_t* row = a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32;
+    *reinterpret_cast<uint2*>(row + pos) = make_uint2(w0, w1);
+    if (l8 == 0) {
+        a.d[(int64_t)b * a.Tpad + t] = dd;
+        a.ds[(int64_t)b * a.Tpad + t] = dd * (float)sum;
     }
-    uint4* dst = reinterpret_cast<uint4*>(a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32);
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-    dst[2] = make_uint4(w[8], w[9], w[10], w[11]);
-    dst[3] = make_uint4(w[12], w[13], w[14], w[15]);
-    a.d[(int64_t)b * a.Tpad + t] = dd;
-    a.ds[(int64_t)b * a.Tpad + t] = ds;
 }
 
-__device__ inline void store_zero_block(const ActQ8& a, int t, int b)
+__device__ __forceinline__ void zero_block8(int l8, const ActQ8& a, int t, int b)
 {
-    uint4* dst = reinterpret_cast<uint4*>(a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32);
-    for (int k = 0; k < 4; k++) dst[k] = make_uint4(0, 0, 0, 0);
-    a.d[(int64_t)b * a.Tpad + t] = 0.0f;
-    a.ds[(int64_t)b * a.Tpad + t] = 0.0f;
-}
-
-__global__ void k_quant_act(const float* __restrict__ x, int ldx, ActQ8 a, int semantics)
-{
-    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)a.Tpad * a.B) return;
-    int t = (int)(idx % a.Tpad), b = (int)(idx / a.Tpad);
-    if (t >= a.T) { store_zero_block(a, t, b); return; }
-    float v[32];
-    const float4* src = reinterpret_cast<const float4*>(x + (int64_t)t * ldx + 32 * b);
-    for (int k = 0; k < 8; k++) {
-        float4 f = src[k];
-        v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    uint16_t* row = a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32;
+    *reinterpret_cast<uint2*>(row + 4 * l8) = make_uint2(0u, 0u);
+    if (l8 == 0) {
+        a.d[(int64_t)b * a.Tpad + t] = 0.0f;
+        a.ds[(int64_t)b * a.Tpad + t] = 0.0f;
     }
-    int8_t q[32];
-    float dd, ds;
-    quant32(v, semantics, q, dd, ds);
-    store_q8_block(a, t, b, q, dd, ds);
+}
+
+// IntegerGemm.QuantizeActivations over x[T × K] (semantics 0) or IntegerDot's variant (1):
+// 8 lanes per 32-block, blocks of a token row adjacent across lane groups (coalesced).
+__global__ __launch_bounds__(256) void k_quant_act(const float* __restrict__ x, int ldx, ActQ8 a, int semantics,
+                                                   bool vec)
+{
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t g = idx >> 3;
+    const int l8 = (int)(idx & 7);
+    if (g >= (int64_t)a.Tpad * a.B) return;
+    const int b = (int)(g % a.B), t = (int)(g / a.B);
+    if (t >= a.T) {
+        zero_block8(l8, a, t, b);
+        return;
+    }
+    const float* src = x + (int64_t)t * ldx + 32 * b + 4 * l8;
+    const float4 v = vec ? *reinterpret_cast<const float4*>(src) : make_float4(src[0], src[1], src[2], src[3]);
+    quant_block8(v, l8, a, t, b, semantics);
 }
 
 hipError_t launch_quant_act(const float* x, int ldx, const ActQ8& a, int semantics, hipStream_t s)
 {
-    int64_t n = (int64_t)a.Tpad * a.B;
-    hipLaunchKernelGGL(k_quant_act, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, ldx, a, semantics);
+    const int64_t n = (int64_t)a.Tpad * a.B * 8;
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && ((ldx & 3) == 0);
+    hipLaunchKernelGGL(k_quant_act, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, ldx, a, semantics, vec);
     return hipGetLastError();
 }
 
@@ -204,7 +212,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
     __shared__ float s_scale;
     const int t = blockIdx.x, tid = threadIdx.x;
     if (t >= a.T) {
-        for (int b = tid; b < a.B; b += blockDim.x) store_zero_block(a, t, b);
+        for (int b = tid >> 3; b < a.B; b += blockDim.x >> 3) zero_block8(tid & 7, a, t, b);
         return;
     }
     const float* xr = x + (int64_t)t * ldx;
@@ -231,20 +239,18 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
     }
     __syncthreads();
     const float sc = s_scale;
-    for (int b = tid; b < a.B; b += blockDim.x) {
-        float v[32];
-        for (int k = 0; k < 32; k++) {
-            float p = sx[32 * b + k] * sc;
-            v[k] = p * w[32 * b + k];
-        }
-        if (y_opt) {
-            float* yr = y_opt + (int64_t)t * n + 32 * b;
-            for (int k = 0; k < 32; k++) yr[k] = v[k];
-        }
-        int8_t q[32];
-        float dd, ds;
-        quant32(v, 0, q, dd, ds);
-        store_q8_block(a, t, b, q, dd, ds);
+    const int l8 = tid & 7;
+    for (int b = tid >> 3; b < a.B; b += blockDim.x >> 3) {  // uniform per 8-lane group
+        const int e = 32 * b + 4 * l8;
+        const float4 xv = *reinterpret_cast<const float4*>(sx + e);
+        const float4 wv = *reinterpret_cast<const float4*>(w + e);
+        float4 v;
+        v.x = (xv.x * sc) * wv.x;
+        v.y = (xv.y * sc) * wv.y;
+        v.z = (xv.z * sc) * wv.z;
+        v.w = (xv.w * sc) * wv.w;
+        if (y_opt) *reinterpret_cast<float4*>(y_opt + (int64_t)t * n + e) = v;
+        quant_block8(v, l8, a, t, b, 0);
     }
 }
 
@@ -260,35 +266,35 @@ __device__ __forceinline__ float det_expf(float x);
 // ------------------------------------------------------- SwiGLU + quantize
 
 // Kernels.SwiGlu (Kernels.cs:83-90): gu = g·u, s = 1/(1+e^−g), y = s·gu; then the
-// 32-block quantization of y for the down projection. gu rows hold [gate | up].
-__global__ void k_swiglu_quant(const float* __restrict__ gu, int ldgu, int ffn, ActQ8 a, float* __restrict__ y_opt)
+// 32-block quantization of y for the down projection. gu rows hold [gate | up]. 8 lanes per
+// block, 4 consecutive features per lane, blocks of a token adjacent across lane groups.
+__global__ __launch_bounds__(256) void k_swiglu_quant(const float* __restrict__ gu, int ldgu, int ffn, ActQ8 a,
+                                                      float* __restrict__ y_opt)
 {
-    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)a.Tpad * a.B) return;
-    int t = (int)(idx % a.Tpad), b = (int)(idx / a.Tpad);
-    if (t >= a.T) { store_zero_block(a, t, b); return; }
-    const float* g = gu + (int64_t)t * ldgu + 32 * b;
-    const float* u = g + ffn;
-    float v[32];
-    for (int k = 0; k < 32; k++) {
-        float gv = g[k];
-        float prod = gv * u[k];
-        float sg = 1.0f / (1.0f + det_expf(-gv));
-        v[k] = sg * prod;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t g = idx >> 3;
+    const int l8 = (int)(idx & 7);
+    if (g >= (int64_t)a.Tpad * a.B) return;
+    const int b = (int)(g % a.B), t = (int)(g / a.B);
+    if (t >= a.T) {
+        zero_block8(l8, a, t, b);
+        return;
     }
-    if (y_opt) {
-        float* yr = y_opt + (int64_t)t * ffn + 32 * b;
-        for (int k = 0; k < 32; k++) yr[k] = v[k];
-    }
-    int8_t q[32];
-    float dd, ds;
-    quant32(v, 0, q, dd, ds);
-    store_q8_block(a, t, b, q, dd, ds);
+    const int f = 32 * b + 4 * l8;
+    const float4 gv = *reinterpret_cast<const float4*>(gu + (int64_t)t * ldgu + f);
+    const float4 uv = *reinterpret_cast<const float4*>(gu + (int64_t)t * ldgu + ffn + f);
+    float4 v;
+    v.x = (1.0f / (1.0f + det_expf(-gv.x))) * (gv.x * uv.x);
+    v.y = (1.0f / (1.0f + det_expf(-gv.y))) * (gv.y * uv.y);
+    v.z = (1.0f / (1.0f + det_expf(-gv.z))) * (gv.z * uv.z);
+    v.w = (1.0f / (1.0f + det_expf(-gv.w))) * (gv.w * uv.w);
+    if (y_opt) *reinterpret_cast<float4*>(y_opt + (int64_t)t * ffn + f) = v;
+    quant_block8(v, l8, a, t, b, 0);
 }
 
 hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& a, float* y_opt, hipStream_t s)
 {
-    int64_t n = (int64_t)a.Tpad * a.B;
+    const int64_t n = (int64_t)a.Tpad * a.B * 8;
     hipLaunchKernelGGL(k_swiglu_quant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gu, ldgu, ffn, a, y_opt);
     return hipGetLastError();
 }
