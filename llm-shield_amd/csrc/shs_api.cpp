@@ -335,6 +335,11 @@ struct shs_model {
     Buf cos_tab, sin_tab, qscale_tab;
     // Work buffers, grown on demand.
     Buf h, qkv, ctx, gu, tmp, normed, ffn_act, tokens, pos, items, ids, logits, last_rows, lastidx, bkc, bvc, scores;
+    // Attention work placed by place_items: the score kernel's key-tile chunks and the
+    // scratch split into score tiles, per-tile row maxima and row totals.
+    Buf chunks;
+    int n_chunks = 0;
+    int64_t score_floats = 0, pm_floats = 0;
     ActBuf act;
     shs_capture_fn cap_fn = nullptr;
     void* cap_user = nullptr;
@@ -943,8 +948,10 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         }
         {
             Timed tm(m->prof, "attention", 0, m->stream);
-            HIP_TRY(launch_attention(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, c.head_dim,
-                                     scale, ctx, qdim, m->scores.as<float>(), m->stream));
+            float* scr = m->scores.as<float>();
+            HIP_TRY(launch_attention(qkv, ldqkv, kc, vc, cap, items_dev, n_items, m->chunks.as<AttnChunk>(), m->n_chunks,
+                                     c.n_head, c.n_kv_head, c.head_dim, scale, ctx, qdim, scr, scr + m->score_floats,
+                                     scr + m->score_floats + m->pm_floats, m->stream));
         }
         snprintf(name, sizeof name, "blk.%d.attn_weighted", l);
         if (cap_on && cp.observe(name, ctx, qdim, T, qdim) != SHS_OK) return SHS_E_DEVICE;
@@ -1043,19 +1050,36 @@ std::vector<AttnItem> causal_items(int q_begin, int n, int key_start, int pos0)
     return v;
 }
 
-// Gives every item its own region of the score scratch (4 waves per KV head, one
-// 32×32 tile of 1024 floats per key tile) and makes sure the scratch is large enough.
+// Gives every item its own region of the score scratch (4 waves per KV head, one 32×32
+// tile of 1024 floats per key tile), splits the items' key tiles into the score kernel's
+// chunks (longest items first, so they start first) and sizes the scratch: score tiles,
+// then 32 row maxima per tile, then 32 row totals per (item, KV head, wave).
 shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
 {
+    constexpr int kChunk = 4;
     int64_t off = 0;
     for (auto& it : items) {
         it.s_off = off;
         int64_t n_kt = (it.pos0 + it.q_count + 31) / 32;
         off += n_kt * 1024 * (int64_t)m->cfg.n_kv_head * 4;
     }
-    HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off, 1)));
+    std::vector<AttnChunk> chunks;
+    for (int i = (int)items.size() - 1; i >= 0; i--) {
+        const int n_kt = (items[i].pos0 + items[i].q_count + 31) / 32;
+        for (int k = 0; k < n_kt; k += kChunk) chunks.push_back({i, k, std::min(kChunk, n_kt - k), 0});
+    }
+    m->score_floats = off;
+    m->pm_floats = off / 32;
+    const int64_t tot_floats = (int64_t)items.size() * m->cfg.n_kv_head * 4 * 32;
+    HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off + m->pm_floats + tot_floats, 1)));
     HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
     HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(m->chunks.ensure(sizeof(AttnChunk) * std::max<size_t>(chunks.size(), 1)));
+    HIP_TRY(hipMemcpyAsync(m->chunks.p, chunks.data(), sizeof(AttnChunk) * chunks.size(), hipMemcpyHostToDevice,
+                           m->stream));
+    m->n_chunks = (int)chunks.size();
+    // The host vectors go out of scope: wait for the copies.
+    HIP_TRY(hipStreamSynchronize(m->stream));
     return SHS_OK;
 }
 

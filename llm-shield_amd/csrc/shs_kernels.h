@@ -43,9 +43,16 @@ struct ActQ8 {
 // sequence, whose first query sits at position pos0 and whose keys live at cache
 // index key_start + p for p in [0, pos0 + q_count). Scores of the item's heads go to
 // scratch + s_off.
+// One attention work item: q_count ≤ 32 queries at rows q_start.. of q/ctx, attending to
+// keys key_start .. key_start + pos0 + q_count − 1 of the cache (query i sees pos0 + i + 1).
 struct AttnItem {
     int q_start, q_count, key_start, pos0;
-    int64_t s_off;  // this item's float offset in the score scratch (n_head · n_tiles · 1024 floats)
+    int64_t s_off;  // float offset of the item's score tiles: n_kv · 4 · n_tiles tiles of 1024 floats
+};
+
+// A run of ≤ 4 key tiles of one item, the unit of the score kernel.
+struct AttnChunk {
+    int item, kt0, nkt, pad;
 };
 
 enum GemmMode { GEMM_STORE = 0, GEMM_ADD = 1 };
@@ -71,8 +78,9 @@ hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv_
                              const float* qscale_tab, int half, float* kc, float* vc, int cap,
                              int kv_slot0, hipStream_t s);
 hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap,
-                            const AttnItem* items, int n_items, int n_head, int n_kv_head, int head_dim,
-                            float scale, float* ctx, int ldc, float* scratch, hipStream_t s);
+                            const AttnItem* items, int n_items, const AttnChunk* chunks, int n_chunks, int n_head,
+                            int n_kv_head, int head_dim, float scale, float* ctx, int ldc, float* scratch, float* pm,
+                            float* tot, hipStream_t s);
 hipError_t launch_expf(const float* x, int n, float* y, hipStream_t s);
 hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s);
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);

@@ -860,41 +860,45 @@ __device__ __forceinline__ float det_expf(float x)
 //  * score = (Σ over 8 lanes of a 16-step FMA chain q[l+8m]·k[l+8m], summed pairwise)·scale
 //    — Kernels.Dot4 with Vector<float>.Count = 8;
 //  * softmax: max, e = exp(s − max), Σe over 8 strided lanes (pairwise) then the tail in
-//    order, w = e / Σe;
+//    order, w = e / Σe; a row whose max is not finite becomes uniform (e = 1, Σe = n);
 //  * ctx[d] = fma(v[p][d], w[p], ctx[d]) for p = 0, 1, 2, … — Kernels.AddScaled4.
 // v_mfma_f32_32x32x2f32 computes fma(a1, b1, fma(a0, b0, c)) per element, so each
-// instruction is two consecutive steps of those FMA chains for a 32×32 tile. A block holds
-// the 4 query heads of one KV head for ≤ 32 queries; K and V tiles are staged in LDS.
-// Three passes over the keys: scores (kept in a scratch buffer) and their max; the sum of
-// exponentials; the weighted values. The score tile's rows are keys permuted so that lane
-// half h holds the keys of parity h, which lets the value pass consume register c of both
-// halves as the key pair (2c, 2c+1).
+// instruction is two consecutive steps of those FMA chains for a 32×32 tile.
+// Three kernels, each parallel over what its step allows:
+//  1. scores: one block per (item, chunk of ≤ 4 key tiles, KV head), a wave per query head;
+//     each 32×32 score tile goes to the scratch with its per-row max;
+//  2. softmax: one block per (item, KV head): e overwrites the scores, Σe goes to a row buffer;
+//  3. values: one block per (item, 32-dimension slice, KV head): w = e / Σe and the ordered
+//     FMA chain over the keys.
+// A score tile is stored in the MFMA's D layout with its rows permuted: lane j + 32h,
+// register r holds query j and key 2r + h of the tile (the A operand's row i carries key
+// kap(i) = 8(i/8) + 2(i%4) + (i%8)/4), so the value step feeds register c of both lane
+// halves to the MFMA as the key pair (2c, 2c+1).
 constexpr int ATT_HD = 128;
 
-__global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
-                                                   const float* __restrict__ vc, int cap,
-                                                   const AttnItem* __restrict__ items, int n_items, int n_head,
-                                                   int n_kv, float scale, float* __restrict__ ctx, int ldc,
-                                                   float* __restrict__ scratch)
+__device__ __forceinline__ int att_tiles(const AttnItem& it) { return (it.pos0 + it.q_count + 31) >> 5; }
+
+__global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
+                                                     int cap, const AttnItem* __restrict__ items,
+                                                     const AttnChunk* __restrict__ chunks, int n_head, int n_kv,
+                                                     float scale, float* __restrict__ scratch, float* __restrict__ pm)
 {
     __shared__ float Ks[ATT_HD * 32];  // [element][key]
-    __shared__ float Vs[32 * ATT_HD];  // [key][dim]
-    __shared__ float tail[4][32][8];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
-    const AttnItem it = items[n_items - 1 - blockIdx.x];
+    const AttnChunk ch = chunks[blockIdx.x];
+    const AttnItem it = items[ch.item];
     const int kvh = blockIdx.y;
     const int group = n_head / n_kv;
     const bool active = wave < group;
     const int head = active ? kvh * group + wave : kvh * group;
-    const float* kb = kc + (int64_t)kvh * cap * ATT_HD;
-    const float* vb = vc + (int64_t)kvh * cap * ATT_HD;
+    const float* kb = kc + ((int64_t)kvh * cap + it.key_start) * ATT_HD;
     const int n_keys = it.pos0 + it.q_count;
-    const int n_kt = (n_keys + 31) >> 5;
-    float* sw = scratch + it.s_off + (int64_t)(kvh * 4 + wave) * n_kt * 1024;
-
+    const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + wave) * att_tiles(it);
     const bool qvalid = active && j < it.q_count;
     const int nq = it.pos0 + j + 1;  // keys this query attends to
+
     // Query elements for the score chains: qv[8l + s] = q[l + 16s + 8h].
     float qv[64];
     {
@@ -904,26 +908,35 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
 #pragma unroll
             for (int s = 0; s < 8; s++) qv[8 * l + s] = qvalid ? qrow[l + 16 * s + 8 * h] : 0.0f;
     }
-    // Score row i of a tile holds key kap(i) = 8(i/8) + 2(i%4) + (i%8)/4.
     const int kap = 8 * (j >> 3) + 2 * (j & 3) + ((j >> 2) & 1);
 
-    // ---- pass 1: scores and their max
-    float mx = -INFINITY;
-    for (int kt = 0; kt < n_kt; ++kt) {
+    float4 kr[4];  // next K tile: thread tid holds key e & 31, elements 4(e >> 5) .. +3 for e = tid + 256i
+    auto kload = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i;
+            const int kidx = kt * 32 + (e & 31);
+            kr[i] = kidx < n_keys ? *reinterpret_cast<const float4*>(kb + (int64_t)kidx * ATT_HD + 4 * (e >> 5))
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    kload(ch.kt0);
+    for (int u = 0; u < ch.nkt; ++u) {
+        const int kt = ch.kt0 + u;
         __syncthreads();
-        for (int e = threadIdx.x; e < 32 * 32; e += blockDim.x) {
-            const int key = e & 31, d4 = e >> 5;
-            const int kidx = kt * 32 + key;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (kidx < n_keys) kv = *reinterpret_cast<const float4*>(kb + (int64_t)(it.key_start + kidx) * ATT_HD + 4 * d4);
-            Ks[(4 * d4 + 0) * 32 + key] = kv.x;
-            Ks[(4 * d4 + 1) * 32 + key] = kv.y;
-            Ks[(4 * d4 + 2) * 32 + key] = kv.z;
-            Ks[(4 * d4 + 3) * 32 + key] = kv.w;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i;
+            const int key = e & 31, d = 4 * (e >> 5);
+            Ks[(d + 0) * 32 + key] = kr[i].x;
+            Ks[(d + 1) * 32 + key] = kr[i].y;
+            Ks[(d + 2) * 32 + key] = kr[i].z;
+            Ks[(d + 3) * 32 + key] = kr[i].w;
         }
         __syncthreads();
+        if (u + 1 < ch.nkt) kload(kt + 1);
         if (!active) continue;
-        v16f acc01, acc23, acc45, acc67;
+        v16f part[4];
 #pragma unroll
         for (int pair = 0; pair < 4; pair++) {
             v16f c0, c1;
@@ -935,51 +948,80 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
                 c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(l0 + 16 * s + 8 * h) * 32 + kap], qv[8 * l0 + s], c0, 0, 0, 0);
                 c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(l1 + 16 * s + 8 * h) * 32 + kap], qv[8 * l1 + s], c1, 0, 0, 0);
             }
-            v16f sum;
 #pragma unroll
-            for (int r = 0; r < 16; r++) sum[r] = c0[r] + c1[r];
-            if (pair == 0) acc01 = sum;
-            else if (pair == 1) acc23 = sum;
-            else if (pair == 2) acc45 = sum;
-            else acc67 = sum;
+            for (int r = 0; r < 16; r++) part[pair][r] = c0[r] + c1[r];
         }
         float sc[16];
+        float mx = -INFINITY;
+        bool nan = false;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const float a = acc01[r] + acc23[r];
-            const float b = acc45[r] + acc67[r];
-            sc[r] = (a + b) * scale;
-            const int key = kt * 32 + 8 * (r >> 2) + 2 * (r & 3) + h;
-            if (qvalid && key < nq) mx = fmaxf(mx, sc[r]);
+            sc[r] = ((part[0][r] + part[1][r]) + (part[2][r] + part[3][r])) * scale;
+            const int key = kt * 32 + 2 * r + h;
+            if (qvalid && key < nq) {
+                mx = fmaxf(mx, sc[r]);
+                nan = nan || sc[r] != sc[r];
+            }
         }
-        float4* out = reinterpret_cast<float4*>(sw + ((int64_t)kt * 64 + lane) * 16);
+        float4* out = reinterpret_cast<float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
 #pragma unroll
         for (int g = 0; g < 4; g++) out[g] = make_float4(sc[4 * g], sc[4 * g + 1], sc[4 * g + 2], sc[4 * g + 3]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        nan = nan || __shfl_xor((int)nan, 32);
+        if (h == 0) pm[(tile0 + kt) * 32 + j] = nan ? __builtin_nanf("") : mx;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+}
 
-    // ---- pass 2: Σ exp(s − max) over 8 strided lanes, pairwise, then the tail in order
+__global__ __launch_bounds__(256) void k_attn_softmax(const AttnItem* __restrict__ items, int n_items, int n_head,
+                                                      int n_kv, float* __restrict__ scratch, const float* __restrict__ pm,
+                                                      float* __restrict__ tot)
+{
+    __shared__ float tail[4][32][8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 31, h = lane >> 5;
+    const int idx = n_items - 1 - blockIdx.x;
+    const AttnItem it = items[idx];
+    const int kvh = blockIdx.y;
+    const bool active = wave < n_head / n_kv;
+    const int n_kt = att_tiles(it);
+    const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + wave) * n_kt;
+    const bool qvalid = active && j < it.q_count;
+    const int nq = it.pos0 + j + 1;
     const int n8 = nq & ~7;
-    float L[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // residues 2t + h
-    if (active) {
+
+    float mx = -INFINITY;
+    bool nan = false;
+    if (qvalid)
         for (int kt = 0; kt < n_kt; ++kt) {
-            const float4* in = reinterpret_cast<const float4*>(sw + ((int64_t)kt * 64 + lane) * 16);
+            const float v = pm[(tile0 + kt) * 32 + j];
+            mx = fmaxf(mx, v);
+            nan = nan || v != v;
+        }
+    const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);  // Kernels.Softmax: a non-finite max
+    float L[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // residues 2t + h
+    if (active)
+        for (int kt = 0; kt < n_kt; ++kt) {
+            float4* io = reinterpret_cast<float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
             float sc[16];
 #pragma unroll
             for (int g = 0; g < 4; g++) {
-                const float4 v = in[g];
+                const float4 v = io[g];
                 sc[4 * g] = v.x; sc[4 * g + 1] = v.y; sc[4 * g + 2] = v.z; sc[4 * g + 3] = v.w;
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int key = kt * 32 + 8 * (r >> 2) + 2 * (r & 3) + h;
-                if (!qvalid || key >= nq) continue;
-                const float e = det_expf(sc[r] - mx);
-                if (key < n8) L[r & 3] = L[r & 3] + e;
-                else tail[wave][j][key - n8] = e;
+                const int key = kt * 32 + 2 * r + h;
+                const bool valid = qvalid && key < nq;
+                const float e = valid ? (uniform ? 1.0f : det_expf(sc[r] - mx)) : 0.0f;
+                if (valid) {
+                    if (key < n8) L[r & 3] = L[r & 3] + e;
+                    else tail[wave][j][key - n8] = e;
+                }
+                sc[r] = e;
             }
+#pragma unroll
+            for (int g = 0; g < 4; g++) io[g] = make_float4(sc[4 * g], sc[4 * g + 1], sc[4 * g + 2], sc[4 * g + 3]);
         }
-    }
     float other[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) other[t] = __shfl_xor(L[t], 32);
@@ -991,63 +1033,80 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     }
     float total = ((a8[0] + a8[1]) + (a8[2] + a8[3])) + ((a8[4] + a8[5]) + (a8[6] + a8[7]));
     __syncthreads();
-    if (qvalid)
+    if (qvalid && h == 0) {
         for (int p = 0; p < nq - n8; p++) total = total + tail[wave][j][p];
+        tot[((int64_t)idx * n_kv * 4 + kvh * 4 + wave) * 32 + j] = total;
+    }
+}
 
-    // ---- pass 3: ctx = Σ_p fma(v[p], w[p], ctx) in position order
-    v16f o[4];
+__global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, int cap, const AttnItem* __restrict__ items,
+                                                 int n_items, int n_head, int n_kv, const float* __restrict__ scratch,
+                                                 const float* __restrict__ tot, float* __restrict__ ctx, int ldc)
+{
+    __shared__ float Vs[2][32 * 32];  // [key][dimension within the slice]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 31, h = lane >> 5;
+    const int idx = n_items - 1 - (int)(blockIdx.x >> 2);
+    const int dt = blockIdx.x & 3;
+    const AttnItem it = items[idx];
+    const int kvh = blockIdx.y;
+    const int group = n_head / n_kv;
+    const bool active = wave < group;
+    const int head = active ? kvh * group + wave : kvh * group;
+    const int n_keys = it.pos0 + it.q_count;
+    const int n_kt = att_tiles(it);
+    const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + wave) * n_kt;
+    const bool qvalid = active && j < it.q_count;
+    const float total = qvalid ? tot[((int64_t)idx * n_kv * 4 + kvh * 4 + wave) * 32 + j] : 1.0f;
+    const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD + 32 * dt;
+
+    const int vkey = tid >> 3, vd = 4 * (tid & 7);  // thread tid stages key vkey, dimensions vd .. vd+3
+    auto vload = [&](int kt) {
+        const int kidx = kt * 32 + vkey;
+        return kidx < n_keys ? *reinterpret_cast<const float4*>(vb + (int64_t)kidx * ATT_HD + vd)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    v16f o;
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) o[dt][r] = 0.0f;
+    for (int r = 0; r < 16; r++) o[r] = 0.0f;
+    float4 vr = vload(0);
     for (int kt = 0; kt < n_kt; ++kt) {
+        const int buf = kt & 1;
+        *reinterpret_cast<float4*>(&Vs[buf][vkey * 32 + vd]) = vr;
         __syncthreads();
-        for (int e = threadIdx.x; e < 32 * 32; e += blockDim.x) {
-            const int key = e & 31, d4 = e >> 5;
-            const int kidx = kt * 32 + key;
-            float4 vv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (kidx < n_keys) vv = *reinterpret_cast<const float4*>(vb + (int64_t)(it.key_start + kidx) * ATT_HD + 4 * d4);
-            *reinterpret_cast<float4*>(&Vs[key * ATT_HD + 4 * d4]) = vv;
+        if (kt + 1 < n_kt) vr = vload(kt + 1);
+        if (active) {
+            const float4* in = reinterpret_cast<const float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
+            float w[16];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const float4 v = in[g];
+                w[4 * g] = v.x / total; w[4 * g + 1] = v.y / total; w[4 * g + 2] = v.z / total; w[4 * g + 3] = v.w / total;
+            }
+#pragma unroll
+            for (int c = 0; c < 16; c++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][(2 * c + h) * 32 + j], w[c], o, 0, 0, 0);
         }
-        __syncthreads();
-        if (!active) continue;
-        const float4* in = reinterpret_cast<const float4*>(sw + ((int64_t)kt * 64 + lane) * 16);
-        float w[16];
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const float4 v = in[g];
-            w[4 * g] = v.x; w[4 * g + 1] = v.y; w[4 * g + 2] = v.z; w[4 * g + 3] = v.w;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int key = kt * 32 + 8 * (r >> 2) + 2 * (r & 3) + h;
-            w[r] = (qvalid && key < nq) ? det_expf(w[r] - mx) / total : 0.0f;
-        }
-#pragma unroll
-        for (int c = 0; c < 16; c++)
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(2 * c + h) * ATT_HD + 32 * dt + j], w[c], o[dt], 0, 0, 0);
     }
     if (!qvalid) return;
-    float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD;
+    float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD + 32 * dt;
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int dim = 32 * dt + 8 * g + 4 * h;
-            *reinterpret_cast<float4*>(outp + dim) =
-                make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
-        }
+    for (int g = 0; g < 4; g++)
+        *reinterpret_cast<float4*>(outp + 8 * g + 4 * h) = make_float4(o[4 * g], o[4 * g + 1], o[4 * g + 2], o[4 * g + 3]);
 }
 
 hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
-                            int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
-                            float* scratch, hipStream_t s)
+                            int n_items, const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim,
+                            float scale, float* ctx, int ldc, float* scratch, float* pm, float* tot, hipStream_t s)
 {
     if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attention, dim3(n_items, n_kv), dim3(256), 0, s, q, ldq, kc, vc, cap, items, n_items, n_head,
-                       n_kv, scale, ctx, ldc, scratch);
+    if (n_items <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_attn_scores, dim3(n_chunks, n_kv), dim3(256), 0, s, q, ldq, kc, cap, items, chunks, n_head,
+                       n_kv, scale, scratch, pm);
+    hipLaunchKernelGGL(k_attn_softmax, dim3(n_items, n_kv), dim3(256), 0, s, items, n_items, n_head, n_kv, scratch, pm,
+                       tot);
+    hipLaunchKernelGGL(k_attn_pv, dim3(4 * n_items, n_kv), dim3(256), 0, s, vc, cap, items, n_items, n_head, n_kv,
+                       scratch, tot, ctx, ldc);
     return hipGetLastError();
 }
 
