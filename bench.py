@@ -23,23 +23,32 @@ METRIC = "prefill tok/s + ms/verdict (1k-token prompt), Shieldstral-3B Q4_0, 1 M
 T_PROMPT = 1024
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0
-# The roofline kernel: the fused gate|up projection (18432 x 3072, Q4_0), the largest GEMM
-# of a layer and the only launch of its kernel instantiation.
-ROOF_CLASS = "gemm_gate_up"
-ROOF_KERNEL = "k_gemm<Q4_0, TT=4, STORE>: fused gate|up 18432x3072 Q4_0 weights x 1024 Q8 tokens"
-# HBM bytes per launch of that kernel from rocprofv3 FETCH_SIZE / WRITE_SIZE passes,
-# calibrated against a device copy of known size (written by the profiling procedure).
-TRAFFIC_FILE = ROOT / "profiles" / "k_gemm_gate_up_q4_0_t1024_traffic.md"
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+TYPE_NAMES = {2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8: "Q8_0"}
+# The roofline is quoted for the GEMM kernel instantiation (k_gemm<type,TT,mode>, the name
+# rocprofv3 reports) with the most time in the timed region. HBM bytes per launch come
+# from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over that kernel, calibrated against a
+# device copy of known size, recorded in profiles/<kernel>_traffic.md.
 COPY_PROBE_BYTES = 256 << 20
 
 
-def read_traffic():
+def traffic_file(kernel):
+    return ROOT / "profiles" / (kernel.replace("<", "_").replace(">", "").replace(",", "_") + "_traffic.md")
+
+
+def read_traffic(kernel, T):
     try:
-        for line in TRAFFIC_FILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
+        text = traffic_file(kernel).read_text()
+    except OSError:
+        return None
+    if f"tokens: {T}" not in text:
+        return None
+    for line in text.splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
                 return int(line.split(":", 1)[1].strip())
-    except (OSError, ValueError):
-        pass
+            except ValueError:
+                return None
     return None
 
 
@@ -102,6 +111,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=T_PROMPT)
     ap.add_argument("--seed", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true",
+                    help="time without the per-kernel HIP events (no roofline or breakdown)")
     ap.add_argument("--copy-probe", action="store_true",
                     help=f"first copy {COPY_PROBE_BYTES >> 20} MiB device to device (counter calibration)")
     args = ap.parse_args()
@@ -131,30 +142,60 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    # Every library call returns only after its stream has drained, so the region is
-    # bracketed by device synchronisation on both sides. torch is not imported: it
-    # bundles its own HIP/HSA runtime, and two HSA runtimes cannot share one process.
-    model.profile_reset()
-    model.profile(True)
+    # Timed region: K steps bracketed by device synchronisation (every library call also
+    # returns only after its stream has drained). torch is not imported: it bundles its own
+    # HIP/HSA runtime, and two HSA runtimes cannot share one process.
     model.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         result = step()
     model.synchronize()
     elapsed = time.perf_counter() - t0
-    model.profile(False)
     ms = elapsed / args.steps * 1e3
+    if args.no_profile:
+        print(json.dumps({"metric": METRIC, "value": round(T / (ms * 1e-3), 1), "unit": "tok/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+                          "profiled": False}), flush=True)
+        model.close()
+        return 0
+    # Kernel timing: the same K steps again with a HIP event pair recorded on the model's
+    # stream around every launch (the events add gaps between launches, so this pass is
+    # not the one `value` comes from; kernel durations are unaffected).
+    model.profile_reset()
+    model.profile(True)
+    model.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    model.synchronize()
+    ms_profiled = (time.perf_counter() - t1) / args.steps * 1e3
+    model.profile(False)
 
-    n, roof_ms, roof_ops = model.profile_read(ROOF_CLASS)
+    kernels = {}
+    for t in TYPE_NAMES:
+        for tt in (1, 2, 4):
+            for mode in (0, 1):
+                name = f"k_gemm<{t},{tt},{mode}>"
+                c, cms, cops = model.profile_read(name)
+                if c:
+                    kernels[name] = (c, cms, cops)
+    roof_kernel = max(kernels, key=lambda k: kernels[k][1])
+    n, roof_ms, roof_ops = kernels[roof_kernel]
     achieved = roof_ops / (roof_ms * 1e-3) / 1e12 if roof_ms > 0 else 0.0
+    t_, tt_, mode_ = (int(v) for v in roof_kernel[7:-1].split(","))
     breakdown = {}
-    for cls in ("gemm*", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "attention", "rmsnorm_quant",
-                "swiglu_quant", "quant_act", "rope_store", "embed", "gemv"):
+    for cls in ["gemm*", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "attention", "k_attn_scores",
+                "k_attn_softmax", "k_attn_pv", "rmsnorm_quant", "swiglu_quant", "quant_act", "rope_store", "embed",
+                "gemv"] + sorted(kernels):
         c, cms, cops = model.profile_read(cls)
         if c:
-            e = {"launches_per_step": c // args.steps, "ms_per_step": round(cms / args.steps, 4)}
+            e = {"launches_per_step": c // args.steps, "ms_per_step": round(cms / args.steps, 4),
+                 "us_per_launch": round(cms / c * 1e3, 2)}
             if cops:
-                e["tops"] = round(cops / (cms * 1e-3) / 1e12, 1)
+                rate = cops / (cms * 1e-3) / 1e12
+                e["tops"] = round(rate, 1)
+                if cls.startswith("k_attn"):
+                    e["frac_fp32_mfma"] = round(rate / PEAK_FP32_TFLOPS, 4)
             breakdown[cls.rstrip("*") + ("_all" if cls.endswith("*") else "")] = e
 
     line = {
@@ -176,12 +217,15 @@ def main():
                    "layers": cfg.layer_count, "hidden": cfg.hidden_size, "ffn": cfg.feed_forward_size,
                    "heads": cfg.head_count, "kv_heads": cfg.kv_head_count, "vocab": cfg.vocab_size,
                    "tokens": T, "weights": "Q4_0", "seed": args.seed},
-        "roofline": {"bound": "mfma", "kernel": ROOF_KERNEL,
+        "roofline": {"bound": "mfma",
+                     "kernel": f"{roof_kernel}: {TYPE_NAMES[t_]} block-quantized GEMM, {tt_} token tile(s) of 32 per "
+                               f"block, {'add into' if mode_ else 'store to'} the output (int8 ops vs the int8 peak)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": read_traffic(),
+                     "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": read_traffic(roof_kernel, T),
                      "launches": n, "ms_per_launch": round(roof_ms / max(n, 1), 5),
                      "ops_per_launch": round(roof_ops / max(n, 1))},
         "breakdown": breakdown,
+        "ms_per_step_with_kernel_events": round(ms_profiled, 4),
         "score": result.score,
     }
     if not args.no_cpu_baseline:

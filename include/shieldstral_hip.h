@@ -181,9 +181,12 @@ shs_status shs_synchronize(shs_model* model);
 
 /* Per-kernel-class timing with HIP events recorded on the launching stream around
  * every launch of that class while enabled (no counterpart in the reference, whose
- * bench times whole calls, Benchmark.cs:537-611). Classes: gemm_qkv, gemm_o,
+ * bench times whole calls, Benchmark.cs:537-611). Classes by step: gemm_qkv, gemm_o,
  * gemm_gate_up, gemm_down, gemm_head, gemv, attention, rmsnorm_quant, swiglu_quant,
- * quant_act, rope_store, embed. kernel_class "prefix*" sums the classes with that prefix. */
+ * quant_act, rope_store, embed; and by kernel, under the names rocprofv3 reports:
+ * "k_gemm<type,TT,mode>" (each GEMM launch is in both), k_attn_scores, k_attn_softmax,
+ * k_attn_pv. kernel_class "prefix*" sums the classes with that prefix. total_ops is the
+ * algorithmic operation count (2·tokens·rows·cols for a GEMM, 0 where not counted). */
 shs_status shs_profile_enable(shs_model* model, int32_t enable);
 shs_status shs_profile_read(shs_model* model, const char* kernel_class, int64_t* launches,
                             double* total_ms, double* total_ops);

@@ -212,7 +212,7 @@ struct Profiler {
     bool on = false;
     struct Rec {
         hipEvent_t a, b;
-        std::string cls;
+        std::string cls, cls2;  // one event pair, counted under one or two classes
         double ops;
     };
     std::vector<Rec> pending;
@@ -229,11 +229,12 @@ struct Profiler {
         if (hipEventCreate(&e) != hipSuccess) return nullptr;
         return e;
     }
-    void begin(const char* cls, double ops, hipStream_t s, Rec* r)
+    void begin(const char* cls, const char* cls2, double ops, hipStream_t s, Rec* r)
     {
         r->a = get();
         r->b = get();
         r->cls = cls;
+        r->cls2 = cls2 ? cls2 : "";
         r->ops = ops;
         if (r->a) (void)hipEventRecord(r->a, s);
     }
@@ -247,10 +248,13 @@ struct Profiler {
         for (auto& r : pending) {
             float ms = 0.0f;
             if (r.a && r.b && hipEventSynchronize(r.b) == hipSuccess && hipEventElapsedTime(&ms, r.a, r.b) == hipSuccess) {
-                auto& t = totals[r.cls];
-                t.first += 1;
-                t.second.first += ms;
-                t.second.second += r.ops;
+                for (const std::string* c : {&r.cls, &r.cls2}) {
+                    if (c->empty()) continue;
+                    auto& t = totals[*c];
+                    t.first += 1;
+                    t.second.first += ms;
+                    t.second.second += r.ops;
+                }
             }
             if (r.a) pool.push_back(r.a);
             if (r.b) pool.push_back(r.b);
@@ -273,9 +277,10 @@ struct Timed {
     hipStream_t s;
     Profiler::Rec rec{};
     bool active;
-    Timed(Profiler& pr, const char* cls, double ops, hipStream_t st) : p(pr), s(st), active(pr.on)
+    Timed(Profiler& pr, const char* cls, double ops, hipStream_t st, const char* cls2 = nullptr)
+        : p(pr), s(st), active(pr.on)
     {
-        if (active) p.begin(cls, ops, s, &rec);
+        if (active) p.begin(cls, cls2, ops, s, &rec);
     }
     ~Timed()
     {
@@ -336,10 +341,12 @@ struct shs_model {
     // Work buffers, grown on demand.
     Buf h, qkv, ctx, gu, tmp, normed, ffn_act, tokens, pos, items, ids, logits, last_rows, lastidx, bkc, bvc, scores;
     // Attention work placed by place_items: the score kernel's key-tile chunks and the
-    // scratch split into score tiles, per-tile row maxima and row totals.
-    Buf chunks;
+    // scratch split into score tiles and per-tile row maxima.
+    Buf chunks, counters;  // counters: the attention kernels' three work counters
     int n_chunks = 0;
+    int n_cu = 0;          // compute units of the device (persistent kernel sizing)
     int64_t score_floats = 0, pm_floats = 0;
+    int64_t attn_pairs = 0;
     ActBuf act;
     shs_capture_fn cap_fn = nullptr;
     void* cap_user = nullptr;
@@ -623,6 +630,9 @@ shs_status build_model(const shs_config& c, const SpecMap& tm, int device, int i
     };
     hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
     if (e != hipSuccess) return bail(hip_fail(e, "hipStreamCreate"));
+    if ((e = hipDeviceGetAttribute(&m->n_cu, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess)
+        return bail(hip_fail(e, "hipDeviceGetAttribute"));
+    if ((e = m->counters.ensure(64)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(counters)"));
     m->layers.reserve(c.n_layer);
 
     const int qdim = c.n_head * c.head_dim, kvdim = c.n_kv_head * c.head_dim;
@@ -865,11 +875,16 @@ struct Capture {
 
 double gemm_ops(int T, const DevMatrix& w) { return 2.0 * T * (double)w.rows * w.cols; }
 
+// Each launch is timed under the projection's class and under its kernel instantiation,
+// "k_gemm<type,TT,mode>" (the name rocprofv3 reports, so the two can be compared).
 shs_status run_proj(shs_model* m, const Proj& p, const ActQ8& a, float* y, int ldy, int mode, const char* cls)
 {
     for (size_t i = 0; i < p.parts.size(); i++) {
-        Timed tm(m->prof, cls, gemm_ops(a.T, p.parts[i]), m->stream);
-        HIP_TRY(launch_gemm(p.parts[i], a, y + p.col0[i], ldy, mode, m->stream));
+        const DevMatrix& w = p.parts[i];
+        char kname[48] = "k_gemm";
+        if (m->prof.on) snprintf(kname, sizeof kname, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, a, mode), mode);
+        Timed tm(m->prof, cls, gemm_ops(a.T, w), m->stream, kname);
+        HIP_TRY(launch_gemm(w, a, y + p.col0[i], ldy, mode, m->stream));
     }
     return SHS_OK;
 }
@@ -947,11 +962,25 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             if (cp.observe(name, qkv + qdim + kvdim, ldqkv, T, kvdim) != SHS_OK) return SHS_E_DEVICE;
         }
         {
-            Timed tm(m->prof, "attention", 0, m->stream);
             float* scr = m->scores.as<float>();
-            HIP_TRY(launch_attention(qkv, ldqkv, kc, vc, cap, items_dev, n_items, m->chunks.as<AttnChunk>(), m->n_chunks,
-                                     c.n_head, c.n_kv_head, c.head_dim, scale, ctx, qdim, scr, scr + m->score_floats,
-                                     scr + m->score_floats + m->pm_floats, m->stream));
+            float* pm = scr + m->score_floats;
+            int* ctr = m->counters.as<int>();
+            // 2·head_dim flops per (query, key) pair and head, for the scores and again for the values
+            const double attn_ops = 2.0 * c.head_dim * c.n_head * (double)m->attn_pairs;
+            {
+                Timed tk(m->prof, "k_attn_scores", attn_ops, m->stream, "attention");
+                HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(), m->n_chunks,
+                                           c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, ctr, m->n_cu, m->stream));
+            }
+            {
+                Timed tk(m->prof, "k_attn_softmax", 0, m->stream, "attention");
+                HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu, m->stream));
+            }
+            {
+                Timed tk(m->prof, "k_attn_pv", attn_ops, m->stream, "attention");
+                HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim, ctr, m->n_cu,
+                                       m->stream));
+            }
         }
         snprintf(name, sizeof name, "blk.%d.attn_weighted", l);
         if (cap_on && cp.observe(name, ctx, qdim, T, qdim) != SHS_OK) return SHS_E_DEVICE;
@@ -1053,7 +1082,7 @@ std::vector<AttnItem> causal_items(int q_begin, int n, int key_start, int pos0)
 // Gives every item its own region of the score scratch (4 waves per KV head, one 32×32
 // tile of 1024 floats per key tile), splits the items' key tiles into the score kernel's
 // chunks (longest items first, so they start first) and sizes the scratch: score tiles,
-// then 32 row maxima per tile, then 32 row totals per (item, KV head, wave).
+// then 32 row maxima per tile.
 shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
 {
     constexpr int kChunk = 4;
@@ -1070,8 +1099,9 @@ shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
     }
     m->score_floats = off;
     m->pm_floats = off / 32;
-    const int64_t tot_floats = (int64_t)items.size() * m->cfg.n_kv_head * 4 * 32;
-    HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off + m->pm_floats + tot_floats, 1)));
+    m->attn_pairs = 0;  // (query, key) pairs the items attend over
+    for (const auto& it : items) m->attn_pairs += (int64_t)it.q_count * it.pos0 + (int64_t)it.q_count * (it.q_count + 1) / 2;
+    HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off + m->pm_floats, 1)));
     HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
     HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
     HIP_TRY(m->chunks.ensure(sizeof(AttnChunk) * std::max<size_t>(chunks.size(), 1)));

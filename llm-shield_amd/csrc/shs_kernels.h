@@ -69,6 +69,8 @@ hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float e
                                 float* y_opt, hipStream_t s);
 hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& a, float* y_opt, hipStream_t s);
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s);
+// The token tiles per block launch_gemm picks for this shape (the k_gemm instantiation's TT).
+int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode);
 hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* out, hipStream_t s);
 hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* row_ids, int n_ids, float* y,
                             hipStream_t s);
@@ -77,10 +79,15 @@ hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv_
                              const int32_t* pos, const float* cos_tab, const float* sin_tab,
                              const float* qscale_tab, int half, float* kc, float* vc, int cap,
                              int kv_slot0, hipStream_t s);
-hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap,
-                            const AttnItem* items, int n_items, const AttnChunk* chunks, int n_chunks, int n_head,
-                            int n_kv_head, int head_dim, float scale, float* ctx, int ldc, float* scratch, float* pm,
-                            float* tot, hipStream_t s);
+// Causal GQA attention in three launches on one stream (scores, softmax, values); the
+// first clears the three work counters (counters[0..2]) the launches share.
+hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap, const AttnItem* items,
+                              const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim, float scale,
+                              float* scratch, float* pm, int* counters, int n_cu, hipStream_t s);
+hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, int n_kv, float* scratch, const float* pm,
+                               int* counters, int n_cu, hipStream_t s);
+hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
+                          const float* scratch, float* ctx, int ldc, int* counters, int n_cu, hipStream_t s);
 hipError_t launch_expf(const float* x, int n, float* y, hipStream_t s);
 hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s);
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);

@@ -585,25 +585,90 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
     }
 }
 
-template <int TYPE, int TT>
-static hipError_t gemm_tt(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+template <int TYPE, int TT, int MODE>
+static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
 {
     dim3 grid((unsigned)((w.tiles + 3) / 4), (unsigned)(((a.Tpad >> 5) + TT - 1) / TT)), block(256);
-    if (mode == GEMM_ADD)
-        hipLaunchKernelGGL((k_gemm<TYPE, TT, GEMM_ADD>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy, w.rows);
-    else
-        hipLaunchKernelGGL((k_gemm<TYPE, TT, GEMM_STORE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy, w.rows);
+    hipLaunchKernelGGL((k_gemm<TYPE, TT, MODE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy, w.rows);
     return hipGetLastError();
 }
 
-// Token tiles per block: the largest of 4/2/1 that still gives ≥ 512 blocks (two per CU).
+// Resident blocks of k_gemm<TYPE, TT, MODE> on the whole device (blocks per CU × CUs),
+// asked of the runtime once per instantiation and device.
+template <int TYPE, int TT, int MODE>
+static int gemm_slots()
+{
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] == 0) {
+        int per_cu = 0, n_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm<TYPE, TT, MODE>, 256, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        cached[dev] = per_cu * n_cu;
+    }
+    return cached[dev];
+}
+
+// Token tiles per block: the largest TT of 4/2/1 whose blocks fill their last round of
+// resident slots to ≥ 90 % (a larger TT decodes each weight block for more tokens, a
+// smaller one has more registers to spare and so more resident blocks).
+template <int TYPE, int MODE>
+static int gemm_tt_of(const DevMatrix& w, const ActQ8& a);
+
+// Token tiles per block: the largest TT of 4/2/1 whose blocks fill their last round of
+// resident slots to ≥ 90 % (a larger TT decodes each weight block for more tokens, a
+// smaller one has more registers to spare and so more resident blocks); between 2 and 1,
+// the better filled, 2 on a tie.
+template <int TYPE, int MODE>
+static hipError_t gemm_mode(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+{
+    switch (gemm_tt_of<TYPE, MODE>(w, a)) {
+    case 4: return gemm_launch<TYPE, 4, MODE>(w, a, y, ldy, s);
+    case 2: return gemm_launch<TYPE, 2, MODE>(w, a, y, ldy, s);
+    default: return gemm_launch<TYPE, 1, MODE>(w, a, y, ldy, s);
+    }
+}
+
 template <int TYPE>
 static hipError_t gemm_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
 {
+    return mode == GEMM_ADD ? gemm_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s) : gemm_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s);
+}
+
+template <int TYPE, int MODE>
+static int gemm_tt_of(const DevMatrix& w, const ActQ8& a)
+{
     const int ntt = a.Tpad >> 5, rg = (w.tiles + 3) / 4;
-    if (ntt >= 4 && rg * ((ntt + 3) / 4) >= 512) return gemm_tt<TYPE, 4>(w, a, y, ldy, mode, s);
-    if (ntt >= 2 && rg * ((ntt + 1) / 2) >= 384) return gemm_tt<TYPE, 2>(w, a, y, ldy, mode, s);
-    return gemm_tt<TYPE, 1>(w, a, y, ldy, mode, s);
+    auto fill = [&](int tt, int slots) {
+        const int64_t blocks = (int64_t)rg * ((ntt + tt - 1) / tt);
+        if (slots <= 0) return 0.0;
+        const int64_t rounds = (blocks + slots - 1) / slots;
+        return (double)blocks / (double)(rounds * slots);
+    };
+    if (ntt >= 4 && fill(4, gemm_slots<TYPE, 4, MODE>()) >= 0.9) return 4;
+    if (ntt >= 2 && fill(2, gemm_slots<TYPE, 2, MODE>()) >= 0.9) return 2;
+    if (ntt >= 2 && fill(2, gemm_slots<TYPE, 2, MODE>()) >= fill(1, gemm_slots<TYPE, 1, MODE>())) return 2;
+    return 1;
+}
+
+template <int TYPE>
+static int gemm_tt_type(const DevMatrix& w, const ActQ8& a, int mode)
+{
+    return mode == GEMM_ADD ? gemm_tt_of<TYPE, GEMM_ADD>(w, a) : gemm_tt_of<TYPE, GEMM_STORE>(w, a);
+}
+
+int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode)
+{
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: return gemm_tt_type<SHS_TYPE_Q4_0>(w, a, mode);
+    case SHS_TYPE_Q4_1: return gemm_tt_type<SHS_TYPE_Q4_1>(w, a, mode);
+    case SHS_TYPE_Q5_0: return gemm_tt_type<SHS_TYPE_Q5_0>(w, a, mode);
+    case SHS_TYPE_Q5_1: return gemm_tt_type<SHS_TYPE_Q5_1>(w, a, mode);
+    case SHS_TYPE_Q8_0: return gemm_tt_type<SHS_TYPE_Q8_0>(w, a, mode);
+    default: return 0;
+    }
 }
 
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
@@ -867,9 +932,9 @@ __device__ __forceinline__ float det_expf(float x)
 // Three kernels, each parallel over what its step allows:
 //  1. scores: one block per (item, chunk of ≤ 4 key tiles, KV head), a wave per query head;
 //     each 32×32 score tile goes to the scratch with its per-row max;
-//  2. softmax: one block per (item, KV head): e overwrites the scores, Σe goes to a row buffer;
-//  3. values: one block per (item, 32-dimension slice, KV head): w = e / Σe and the ordered
-//     FMA chain over the keys.
+//  2. softmax: one block per (item, query head): Σe in order, then w = e / Σe over the scores;
+//  3. values: one block per (item, 32-dimension slice, KV head): the ordered FMA chain of w·v
+//     over the keys.
 // A score tile is stored in the MFMA's D layout with its rows permuted: lane j + 32h,
 // register r holds query j and key 2r + h of the tile (the A operand's row i carries key
 // kap(i) = 8(i/8) + 2(i%4) + (i%8)/4), so the value step feeds register c of both lane
@@ -878,18 +943,20 @@ constexpr int ATT_HD = 128;
 
 __device__ __forceinline__ int att_tiles(const AttnItem& it) { return (it.pos0 + it.q_count + 31) >> 5; }
 
-__global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
-                                                     int cap, const AttnItem* __restrict__ items,
-                                                     const AttnChunk* __restrict__ chunks, int n_head, int n_kv,
-                                                     float scale, float* __restrict__ scratch, float* __restrict__ pm)
+// Key-major K tile, rows padded by 4 floats: the 16 lanes of one 16-byte read phase hold
+// 16 different keys, whose rows start 4 banks apart.
+constexpr int ATT_KROW = ATT_HD + 4;
+
+__device__ __forceinline__ void attn_scores_work(const AttnChunk ch, int kvh, const float* __restrict__ q, int ldq,
+                                                 const float* __restrict__ kc, int cap,
+                                                 const AttnItem* __restrict__ items, int n_head, int n_kv, float scale,
+                                                 float* __restrict__ scratch, float* __restrict__ pm, float* Ks)
 {
-    __shared__ float Ks[ATT_HD * 32];  // [element][key]
+    constexpr int KROW = ATT_KROW;
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
-    const AttnChunk ch = chunks[blockIdx.x];
     const AttnItem it = items[ch.item];
-    const int kvh = blockIdx.y;
     const int group = n_head / n_kv;
     const bool active = wave < group;
     const int head = active ? kvh * group + wave : kvh * group;
@@ -899,24 +966,27 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
     const bool qvalid = active && j < it.q_count;
     const int nq = it.pos0 + j + 1;  // keys this query attends to
 
-    // Query elements for the score chains: qv[8l + s] = q[l + 16s + 8h].
-    float qv[64];
+    // B operands: step s of chain l needs q[l + 16s + 8h]; qv[s] holds l = 0..7.
+    float4 qv[8][2];
     {
-        const float* qrow = q + (int64_t)(it.q_start + (qvalid ? j : 0)) * ldq + head * ATT_HD;
+        const float* qrow = q + (int64_t)(it.q_start + (qvalid ? j : 0)) * ldq + head * ATT_HD + 8 * h;
 #pragma unroll
-        for (int l = 0; l < 8; l++)
+        for (int s = 0; s < 8; s++)
 #pragma unroll
-            for (int s = 0; s < 8; s++) qv[8 * l + s] = qvalid ? qrow[l + 16 * s + 8 * h] : 0.0f;
+            for (int x = 0; x < 2; x++)
+                qv[s][x] = qvalid ? *reinterpret_cast<const float4*>(qrow + 16 * s + 4 * x) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    // A operands: row i of the A tile carries key kap(i), so D row i holds key kap(i).
     const int kap = 8 * (j >> 3) + 2 * (j & 3) + ((j >> 2) & 1);
+    const float* krow = Ks + kap * KROW + 8 * h;
 
-    float4 kr[4];  // next K tile: thread tid holds key e & 31, elements 4(e >> 5) .. +3 for e = tid + 256i
+    float4 kr[4];  // next K tile: thread tid holds key e >> 5, elements 4(e & 31) .. +3 for e = tid + 256i
     auto kload = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i;
-            const int kidx = kt * 32 + (e & 31);
-            kr[i] = kidx < n_keys ? *reinterpret_cast<const float4*>(kb + (int64_t)kidx * ATT_HD + 4 * (e >> 5))
+            const int kidx = kt * 32 + (e >> 5);
+            kr[i] = kidx < n_keys ? *reinterpret_cast<const float4*>(kb + (int64_t)kidx * ATT_HD + 4 * (e & 31))
                                   : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
@@ -927,36 +997,39 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i;
-            const int key = e & 31, d = 4 * (e >> 5);
-            Ks[(d + 0) * 32 + key] = kr[i].x;
-            Ks[(d + 1) * 32 + key] = kr[i].y;
-            Ks[(d + 2) * 32 + key] = kr[i].z;
-            Ks[(d + 3) * 32 + key] = kr[i].w;
+            *reinterpret_cast<float4*>(&Ks[(e >> 5) * KROW + 4 * (e & 31)]) = kr[i];
         }
         __syncthreads();
         if (u + 1 < ch.nkt) kload(kt + 1);
         if (!active) continue;
-        v16f part[4];
+        // The 8 chains advance together: step s is 8 independent MFMAs.
+        v16f c[8];
 #pragma unroll
-        for (int pair = 0; pair < 4; pair++) {
-            v16f c0, c1;
+        for (int l = 0; l < 8; l++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) { c0[r] = 0.0f; c1[r] = 0.0f; }
+            for (int r = 0; r < 16; r++) c[l][r] = 0.0f;
 #pragma unroll
-            for (int s = 0; s < 8; s++) {
-                const int l0 = 2 * pair, l1 = 2 * pair + 1;
-                c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(l0 + 16 * s + 8 * h) * 32 + kap], qv[8 * l0 + s], c0, 0, 0, 0);
-                c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(l1 + 16 * s + 8 * h) * 32 + kap], qv[8 * l1 + s], c1, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) part[pair][r] = c0[r] + c1[r];
+        for (int s = 0; s < 8; s++) {
+            const float4 k0 = *reinterpret_cast<const float4*>(krow + 16 * s);
+            const float4 k1 = *reinterpret_cast<const float4*>(krow + 16 * s + 4);
+            c[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.x, qv[s][0].x, c[0], 0, 0, 0);
+            c[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.y, qv[s][0].y, c[1], 0, 0, 0);
+            c[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.z, qv[s][0].z, c[2], 0, 0, 0);
+            c[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.w, qv[s][0].w, c[3], 0, 0, 0);
+            c[4] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.x, qv[s][1].x, c[4], 0, 0, 0);
+            c[5] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.y, qv[s][1].y, c[5], 0, 0, 0);
+            c[6] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.z, qv[s][1].z, c[6], 0, 0, 0);
+            c[7] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.w, qv[s][1].w, c[7], 0, 0, 0);
         }
         float sc[16];
         float mx = -INFINITY;
         bool nan = false;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            sc[r] = ((part[0][r] + part[1][r]) + (part[2][r] + part[3][r])) * scale;
+            // vsum8 of the chains, then the scale
+            const float a = (c[0][r] + c[1][r]) + (c[2][r] + c[3][r]);
+            const float b = (c[4][r] + c[5][r]) + (c[6][r] + c[7][r]);
+            sc[r] = (a + b) * scale;
             const int key = kt * 32 + 2 * r + h;
             if (qvalid && key < nq) {
                 mx = fmaxf(mx, sc[r]);
@@ -972,85 +1045,106 @@ __global__ __launch_bounds__(256) void k_attn_scores(const float* __restrict__ q
     }
 }
 
-__global__ __launch_bounds__(256) void k_attn_softmax(const AttnItem* __restrict__ items, int n_items, int n_head,
-                                                      int n_kv, float* __restrict__ scratch, const float* __restrict__ pm,
-                                                      float* __restrict__ tot)
+// One block per (item, query head); 8 lanes per query row, lane t owning residue t of the
+// row's keys — exactly Kernels.Softmax's Vector<float> lane t, summed in key order.
+__device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnItem* __restrict__ items, int n_head,
+                                                  int n_kv, float* __restrict__ scratch, const float* __restrict__ pm)
 {
-    __shared__ float tail[4][32][8];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int j = lane & 31, h = lane >> 5;
-    const int idx = n_items - 1 - blockIdx.x;
+    const int tid = threadIdx.x;
+    const int j = tid >> 3, t = tid & 7;  // query row j of the item, residue t
     const AttnItem it = items[idx];
-    const int kvh = blockIdx.y;
-    const bool active = wave < n_head / n_kv;
+    const int group = n_head / n_kv;
+    const int kvh = head / group, wave = head % group;  // the score kernel's (KV head, wave)
     const int n_kt = att_tiles(it);
     const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + wave) * n_kt;
-    const bool qvalid = active && j < it.q_count;
+    const bool qvalid = j < it.q_count;
     const int nq = it.pos0 + j + 1;
     const int n8 = nq & ~7;
 
     float mx = -INFINITY;
     bool nan = false;
-    if (qvalid)
-        for (int kt = 0; kt < n_kt; ++kt) {
-            const float v = pm[(tile0 + kt) * 32 + j];
-            mx = fmaxf(mx, v);
-            nan = nan || v != v;
-        }
-    const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);  // Kernels.Softmax: a non-finite max
-    float L[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // residues 2t + h
-    if (active)
-        for (int kt = 0; kt < n_kt; ++kt) {
-            float4* io = reinterpret_cast<float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
-            float sc[16];
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const float4 v = io[g];
-                sc[4 * g] = v.x; sc[4 * g + 1] = v.y; sc[4 * g + 2] = v.z; sc[4 * g + 3] = v.w;
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int key = kt * 32 + 2 * r + h;
-                const bool valid = qvalid && key < nq;
-                const float e = valid ? (uniform ? 1.0f : det_expf(sc[r] - mx)) : 0.0f;
-                if (valid) {
-                    if (key < n8) L[r & 3] = L[r & 3] + e;
-                    else tail[wave][j][key - n8] = e;
-                }
-                sc[r] = e;
-            }
-#pragma unroll
-            for (int g = 0; g < 4; g++) io[g] = make_float4(sc[4 * g], sc[4 * g + 1], sc[4 * g + 2], sc[4 * g + 3]);
-        }
-    float other[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) other[t] = __shfl_xor(L[t], 32);
-    float a8[8];
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        a8[2 * t] = h == 0 ? L[t] : other[t];
-        a8[2 * t + 1] = h == 0 ? other[t] : L[t];
+    for (int kt = t; kt < n_kt; kt += 8) {
+        const float v = pm[(tile0 + kt) * 32 + j];
+        mx = fmaxf(mx, v);
+        nan = nan || v != v;
     }
-    float total = ((a8[0] + a8[1]) + (a8[2] + a8[3])) + ((a8[4] + a8[5]) + (a8[6] + a8[7]));
-    __syncthreads();
-    if (qvalid && h == 0) {
-        for (int p = 0; p < nq - n8; p++) total = total + tail[wave][j][p];
-        tot[((int64_t)idx * n_kv * 4 + kvh * 4 + wave) * 32 + j] = total;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o, 8));
+        nan = nan || __shfl_xor((int)nan, o, 8);
+    }
+    const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);  // Kernels.Softmax: a non-finite max
+
+    // Key t + 8k of a tile sits in lane record j + 32·(t & 1), register (t >> 1) + 4k.
+    const int64_t rec = (int64_t)(j + 32 * (t & 1)) * 16 + (t >> 1);
+    auto expo = [&](float sc, int key) {
+        return key < nq ? (uniform ? 1.0f : det_expf(sc - mx)) : 0.0f;
+    };
+    float lane_sum = 0.0f, tail_e = 0.0f;
+    // Tiles are read in batches of 4 (16 values per lane), the next batch in flight.
+    constexpr int NB = 4;
+    float sv[NB * 4], nx[NB * 4];
+    auto load = [&](int kt0, float* dst) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float* src = scratch + (tile0 + kt0 + b) * 1024 + rec;
+#pragma unroll
+            for (int k = 0; k < 4; k++) dst[4 * b + k] = kt0 + b < n_kt ? src[4 * k] : 0.0f;
+        }
+    };
+    // pass 1: Σe in Kernels.Softmax's order
+    if (qvalid) load(0, nx);
+    for (int kt0 = 0; qvalid && kt0 < n_kt; kt0 += NB) {
+#pragma unroll
+        for (int i = 0; i < NB * 4; i++) sv[i] = nx[i];
+        if (kt0 + NB < n_kt) load(kt0 + NB, nx);
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int key = (kt0 + b) * 32 + t + 8 * k;
+                const float e = expo(sv[4 * b + k], key);
+                if (key < n8) lane_sum = lane_sum + e;
+                else if (key < nq) tail_e = e;
+            }
+    }
+    // vsum8: ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)); addition is commutative, so each lane
+    // forms its pair with its xor partner.
+    float total = lane_sum + __shfl_xor(lane_sum, 1, 8);
+    total = total + __shfl_xor(total, 2, 8);
+    total = total + __shfl_xor(total, 4, 8);
+    // the tail keys n8 .. nq−1 in order; lane k holds key n8 + k
+#pragma unroll
+    for (int k = 0; k < 7; k++) {
+        const float e = __shfl(tail_e, k, 8);
+        if (n8 + k < nq) total = total + e;
+    }
+    // pass 2: w = e / Σe over the scores (e recomputed: the exponential is deterministic),
+    // written over them; keys outside the row get w = 0
+    if (qvalid) load(0, nx);
+    for (int kt0 = 0; qvalid && kt0 < n_kt; kt0 += NB) {
+#pragma unroll
+        for (int i = 0; i < NB * 4; i++) sv[i] = nx[i];
+        if (kt0 + NB < n_kt) load(kt0 + NB, nx);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            if (kt0 + b >= n_kt) break;
+            float* dst = scratch + (tile0 + kt0 + b) * 1024 + rec;
+#pragma unroll
+            for (int k = 0; k < 4; k++) dst[4 * k] = expo(sv[4 * b + k], (kt0 + b) * 32 + t + 8 * k) / total;
+        }
     }
 }
 
-__global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, int cap, const AttnItem* __restrict__ items,
-                                                 int n_items, int n_head, int n_kv, const float* __restrict__ scratch,
-                                                 const float* __restrict__ tot, float* __restrict__ ctx, int ldc)
+__device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const float* __restrict__ vc, int cap,
+                                             const AttnItem* __restrict__ items, int n_head, int n_kv,
+                                             const float* __restrict__ scratch, float* __restrict__ ctx, int ldc,
+                                             float (*Vs)[32 * 32])
 {
-    __shared__ float Vs[2][32 * 32];  // [key][dimension within the slice]
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
-    const int idx = n_items - 1 - (int)(blockIdx.x >> 2);
-    const int dt = blockIdx.x & 3;
     const AttnItem it = items[idx];
-    const int kvh = blockIdx.y;
     const int group = n_head / n_kv;
     const bool active = wave < group;
     const int head = active ? kvh * group + wave : kvh * group;
@@ -1058,7 +1152,6 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, i
     const int n_kt = att_tiles(it);
     const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + wave) * n_kt;
     const bool qvalid = active && j < it.q_count;
-    const float total = qvalid ? tot[((int64_t)idx * n_kv * 4 + kvh * 4 + wave) * 32 + j] : 1.0f;
     const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD + 32 * dt;
 
     const int vkey = tid >> 3, vd = 4 * (tid & 7);  // thread tid stages key vkey, dimensions vd .. vd+3
@@ -1070,23 +1163,38 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, i
     v16f o;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] = 0.0f;
-    float4 vr = vload(0);
-    for (int kt = 0; kt < n_kt; ++kt) {
-        const int buf = kt & 1;
-        *reinterpret_cast<float4*>(&Vs[buf][vkey * 32 + vd]) = vr;
-        __syncthreads();
-        if (kt + 1 < n_kt) vr = vload(kt + 1);
-        if (active) {
-            const float4* in = reinterpret_cast<const float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
-            float w[16];
+    // Two tiles in flight: tile kt's weights and V slice load while tile kt − 2 is multiplied.
+    struct Stage {
+        float4 w[4];  // this lane's weights (keys 2c + h in register c)
+        float4 v;     // the V slice element this thread stages
+    };
+    auto load = [&](int kt, Stage& st) {
+        st.v = vload(kt);
+        const float4* in = reinterpret_cast<const float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const float4 v = in[g];
-                w[4 * g] = v.x / total; w[4 * g + 1] = v.y / total; w[4 * g + 2] = v.z / total; w[4 * g + 3] = v.w / total;
-            }
+        for (int g = 0; g < 4; g++) st.w[g] = active ? in[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto step = [&](int kt, Stage& st) {
+        const int buf = kt & 1;
+        *reinterpret_cast<float4*>(&Vs[buf][vkey * 32 + vd]) = st.v;
+        float w[16];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            w[4 * g] = st.w[g].x; w[4 * g + 1] = st.w[g].y; w[4 * g + 2] = st.w[g].z; w[4 * g + 3] = st.w[g].w;
+        }
+        __syncthreads();
+        if (kt + 2 < n_kt) load(kt + 2, st);
+        if (active) {
 #pragma unroll
             for (int c = 0; c < 16; c++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][(2 * c + h) * 32 + j], w[c], o, 0, 0, 0);
         }
+    };
+    Stage s0, s1;
+    if (n_kt > 0) load(0, s0);
+    if (n_kt > 1) load(1, s1);
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, s0);
+        if (kt + 1 < n_kt) step(kt + 1, s1);
     }
     if (!qvalid) return;
     float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD + 32 * dt;
@@ -1095,18 +1203,93 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, i
         *reinterpret_cast<float4*>(outp + 8 * g + 4 * h) = make_float4(o[4 * g], o[4 * g + 1], o[4 * g + 2], o[4 * g + 3]);
 }
 
-hipError_t launch_attention(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
-                            int n_items, const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim,
-                            float scale, float* ctx, int ldc, float* scratch, float* pm, float* tot, hipStream_t s)
+// The work of each attention kernel is handed out longest first from a counter, one item
+// per block at a time (greedy longest-processing-time order), so that the causal triangle's
+// long rows spread over all CUs whatever the hardware's block placement. Every block leaves
+// its loop once the counter passes the work count.
+__device__ __forceinline__ int next_work(int* counter, int* slot)
+{
+    __syncthreads();  // the block is done with the previous item (and its LDS)
+    if (threadIdx.x == 0) *slot = atomicAdd(counter, 1);
+    __syncthreads();
+    return *slot;
+}
+
+__global__ __launch_bounds__(256, 2) void k_attn_scores(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
+                                                        int cap, const AttnItem* __restrict__ items,
+                                                        const AttnChunk* __restrict__ chunks, int n_chunks, int n_head,
+                                                        int n_kv, float scale, float* __restrict__ scratch,
+                                                        float* __restrict__ pm, int* __restrict__ counter)
+{
+    __shared__ float Ks[32 * ATT_KROW];
+    __shared__ int slot;
+    for (;;) {
+        const int w = next_work(counter, &slot);
+        if (w >= n_chunks * n_kv) break;
+        attn_scores_work(chunks[w / n_kv], w % n_kv, q, ldq, kc, cap, items, n_head, n_kv, scale, scratch, pm, Ks);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_attn_softmax(const AttnItem* __restrict__ items, int n_items, int n_head,
+                                                      int n_kv, float* __restrict__ scratch, const float* __restrict__ pm,
+                                                      int* __restrict__ counter)
+{
+    __shared__ int slot;
+    for (;;) {
+        const int w = next_work(counter, &slot);
+        if (w >= n_items * n_head) break;
+        attn_softmax_work(n_items - 1 - w / n_head, w % n_head, items, n_head, n_kv, scratch, pm);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, int cap, const AttnItem* __restrict__ items,
+                                                 int n_items, int n_head, int n_kv, const float* __restrict__ scratch,
+                                                 float* __restrict__ ctx, int ldc, int* __restrict__ counter)
+{
+    __shared__ float Vs[2][32 * 32];  // [key][dimension within the slice]
+    __shared__ int slot;
+    for (;;) {
+        const int w = next_work(counter, &slot);
+        if (w >= n_items * 4 * n_kv) break;
+        const int per = 4 * n_kv;
+        attn_pv_work(n_items - 1 - w / per, (w % per) / n_kv, (w % per) % n_kv, vc, cap, items, n_head, n_kv, scratch,
+                     ctx, ldc, Vs);
+    }
+}
+
+static dim3 attn_blocks(int n_work, int per_cu, int n_cu)
+{
+    return dim3((unsigned)(n_work < per_cu * n_cu ? n_work : per_cu * n_cu));
+}
+
+hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap, const AttnItem* items,
+                              const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim, float scale,
+                              float* scratch, float* pm, int* counters, int n_cu, hipStream_t s)
 {
     if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4) return hipErrorInvalidValue;
+    if (n_chunks <= 0) return hipSuccess;
+    hipError_t e = launch_fill_zero(reinterpret_cast<float*>(counters), 3, s);  // the three work counters
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_attn_scores, attn_blocks(n_chunks * n_kv, 2, n_cu), dim3(256), 0, s, q, ldq, kc, cap, items,
+                       chunks, n_chunks, n_head, n_kv, scale, scratch, pm, counters);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, int n_kv, float* scratch, const float* pm,
+                               int* counters, int n_cu, hipStream_t s)
+{
     if (n_items <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_attn_scores, dim3(n_chunks, n_kv), dim3(256), 0, s, q, ldq, kc, cap, items, chunks, n_head,
-                       n_kv, scale, scratch, pm);
-    hipLaunchKernelGGL(k_attn_softmax, dim3(n_items, n_kv), dim3(256), 0, s, items, n_items, n_head, n_kv, scratch, pm,
-                       tot);
-    hipLaunchKernelGGL(k_attn_pv, dim3(4 * n_items, n_kv), dim3(256), 0, s, vc, cap, items, n_items, n_head, n_kv,
-                       scratch, tot, ctx, ldc);
+    hipLaunchKernelGGL(k_attn_softmax, attn_blocks(n_items * n_head, 8, n_cu), dim3(256), 0, s, items, n_items, n_head,
+                       n_kv, scratch, pm, counters + 1);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
+                          const float* scratch, float* ctx, int ldc, int* counters, int n_cu, hipStream_t s)
+{
+    if (n_items <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_attn_pv, attn_blocks(n_items * 4 * n_kv, 5, n_cu), dim3(256), 0, s, vc, cap, items, n_items,
+                       n_head, n_kv, scratch, ctx, ldc, counters + 2);
     return hipGetLastError();
 }
 
