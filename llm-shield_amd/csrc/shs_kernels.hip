@@ -737,25 +737,28 @@ __device__ __forceinline__ int weight_elem(const uint8_t* q, uint32_t qh, int e)
     return TYPE == SHS_TYPE_Q4_0 ? u - 8 : TYPE == SHS_TYPE_Q5_0 ? u - 16 : u;
 }
 
-// One thread per (token, selected row): the same exact integer block sums and the same
-// serial epilogue as the GEMM, so every value equals the corresponding entry of the
-// full product bit for bit (QuantMatMul.ForwardRowsAsync, QuantMatMul.cs:98-110).
+// One wave per (token, selected row). The lanes form the exact integer block sums and the
+// scales of all blocks in parallel; lane 0 then runs the serial epilogue over the blocks in
+// order — the GEMM's arithmetic, so every value equals the corresponding entry of the full
+// product bit for bit (QuantMatMul.ForwardRowsAsync, QuantMatMul.cs:98-110).
 template <int TYPE>
-__global__ void k_gemv_rows(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
-                            const float* __restrict__ wd, const float* __restrict__ wm, int B,
-                            const int32_t* __restrict__ ids, int n_ids, ActQ8 a, float* __restrict__ y)
+__global__ __launch_bounds__(64) void k_gemv_rows(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                                                  const float* __restrict__ wd, const float* __restrict__ wm, int B,
+                                                  const int32_t* __restrict__ ids, int n_ids, ActQ8 a,
+                                                  float* __restrict__ y)
 {
     constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
-    int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)a.T * n_ids) return;
-    const int i = (int)(idx % n_ids), t = (int)(idx / n_ids);
+    extern __shared__ float sh[];  // I_b as float (exact), RN(d_w·d_a), then m_w and d_a·Σq for the offset types
+    float* sI = sh;
+    float* sS = sh + B;
+    float* sM = sh + 2 * B;
+    float* sD = sh + 3 * B;
+    const int i = blockIdx.x % n_ids, t = blockIdx.x / n_ids;
     const int r = ids[i];
     const int ri = r & 31;
-    const uint16_t* qa = a.q;
-    float acc = 0.0f;
-    for (int b = 0; b < B; ++b) {
+    for (int b = threadIdx.x; b < B; b += 64) {
         const int64_t rec = (int64_t)(r >> 5) * B + b;
-        const uint16_t* act = qa + (((int64_t)(t >> 5) * B + b) * 32 + (t & 31)) * 32;
+        const uint16_t* act = a.q + (((int64_t)(t >> 5) * B + b) * 32 + (t & 31)) * 32;
         int I = 0;
         if (TYPE == SHS_TYPE_Q8_0) {
             const uint8_t* q = wqs + rec * 1024 + ri * 32;  // stored in the activation order
@@ -766,10 +769,19 @@ __global__ void k_gemv_rows(const uint8_t* __restrict__ wqs, const uint32_t* __r
             for (int p = 0; p < 32; p++)
                 I += weight_elem<TYPE>(q, qh, perm_elem(p)) * (int)__builtin_bit_cast(_Float16, act[p]);
         }
-        const float da = a.d[(int64_t)b * a.Tpad + t];
-        const float sc = wd[rec * 32 + ri] * da;
-        acc = fmaf((float)I, sc, acc);
-        if (OFF) acc = fmaf(wm[rec * 32 + ri], a.ds[(int64_t)b * a.Tpad + t], acc);
+        sI[b] = (float)I;
+        sS[b] = wd[rec * 32 + ri] * a.d[(int64_t)b * a.Tpad + t];
+        if (OFF) {
+            sM[b] = wm[rec * 32 + ri];
+            sD[b] = a.ds[(int64_t)b * a.Tpad + t];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    float acc = 0.0f;
+    for (int b = 0; b < B; ++b) {
+        acc = fmaf(sI[b], sS[b], acc);
+        if (OFF) acc = fmaf(sM[b], sD[b], acc);
     }
     y[(int64_t)t * n_ids + i] = acc;
 }
@@ -777,14 +789,16 @@ __global__ void k_gemv_rows(const uint8_t* __restrict__ wqs, const uint32_t* __r
 hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* ids, int n_ids, float* y,
                             hipStream_t s)
 {
-    int64_t n = (int64_t)a.T * n_ids;
-    dim3 grid((unsigned)((n + 255) / 256)), block(256);
+    const int64_t n = (int64_t)a.T * n_ids;
+    if (n <= 0) return hipSuccess;
+    dim3 grid((unsigned)n), block(64);
+    const size_t shm = sizeof(float) * 4 * (size_t)w.blocks;
     switch (w.type) {
-    case SHS_TYPE_Q4_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q4_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
-    case SHS_TYPE_Q4_1: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q4_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
-    case SHS_TYPE_Q5_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q5_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
-    case SHS_TYPE_Q5_1: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q5_1>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
-    case SHS_TYPE_Q8_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q8_0>, grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q4_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q4_0>, grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q4_1: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q4_1>, grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q5_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q5_0>, grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q5_1: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q5_1>, grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
+    case SHS_TYPE_Q8_0: hipLaunchKernelGGL(k_gemv_rows<SHS_TYPE_Q8_0>, grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.blocks, ids, n_ids, a, y); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
