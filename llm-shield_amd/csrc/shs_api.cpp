@@ -75,21 +75,23 @@ struct Buf {
 };
 
 struct ActBuf {
-    Buf q, d, ds;
+    Buf q, d, cv, ds;
     hipError_t ensure(int T, int K, ActQ8* view)
     {
         int Tpad = (T + 31) / 32 * 32;
         int B = K / 32;
         hipError_t e;
-        if ((e = q.ensure((size_t)Tpad * K * 2)) != hipSuccess) return e;
+        if ((e = q.ensure((size_t)Tpad * K)) != hipSuccess) return e;
         if ((e = d.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
+        if ((e = cv.ensure(sizeof(uint4) * (size_t)Tpad * B)) != hipSuccess) return e;
         if ((e = ds.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
         view->T = T;
         view->Tpad = Tpad;
         view->K = K;
         view->B = B;
-        view->q = q.as<uint16_t>();
+        view->q = q.as<int8_t>();
         view->d = d.as<float>();
+        view->cv = cv.as<uint4>();
         view->ds = ds.as<float>();
         return hipSuccess;
     }

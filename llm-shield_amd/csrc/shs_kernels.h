@@ -9,11 +9,14 @@
 //     d   [tiles][B][32 rows] f32   block scale, fp16 widened exactly
 //     m   [tiles][B][32 rows] f32   block min (Q4_1/Q5_1)
 // Quantized activations (T padded to Tpad, a multiple of 32):
-//     q   [Tpad/32][B][32 tokens][32 fp16]  the int8 values as exact fp16, each block stored
-//                                          in the order [0..7, 16..23, 8..15, 24..31] so MFMA
-//                                          lane half h reads elements 8h.. and 16+8h.. as two
-//                                          16-byte runs (matching the weight nibbles)
+//     q   [Tpad/32][B][2 halves][32 tokens][16 int8]  half h of a token's block holds the
+//                                          elements [8h..8h+7, 16+8h..16+8h+7] — the 16 bytes
+//                                          lane half h of the int8 MFMA multiplies, in the order
+//                                          the weight nibbles unpack to
 //     d   [B][Tpad] f32   scale max|x|/127
+//     cv  [B][Tpad] 16 B  the block's conversion operand: fp16 (−6144, −⌊Σq/64⌋, −(Σq mod 64)),
+//                         then zeros — the B column of the fp16 MFMA that turns the integer
+//                         MFMA's offset sums into exact fp32 block sums (see k_gemm)
 //     ds  [B][Tpad] f32   RN(d·float(Σq)) — the offset types' second factor
 #pragma once
 #include <hip/hip_runtime.h>
@@ -34,8 +37,9 @@ struct DevMatrix {
 
 struct ActQ8 {
     int T = 0, Tpad = 0, K = 0, B = 0;
-    uint16_t* q = nullptr;  // fp16 integer values
+    int8_t* q = nullptr;
     float* d = nullptr;
+    uint4* cv = nullptr;
     float* ds = nullptr;
 };
 

@@ -14,6 +14,7 @@ namespace shs {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 int qs_bytes(int type) { return type == SHS_TYPE_Q8_0 ? 32 : 16; }
 bool type_supported(int t) { return t == 2 || t == 3 || t == 6 || t == 7 || t == 8; }
@@ -106,14 +107,38 @@ hipError_t launch_repack(const DevMatrix& w, const uint8_t* native, int row0, in
 
 // ---------------------------------------------------- activation quantization
 
+// fp16 bit pattern of a small integer (|v| ≤ 2048: exact).
+__device__ __forceinline__ uint32_t half_bits(int v)
+{
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)v);
+}
+
+// The B column of the conversion MFMA for a block with code sum Σq (|Σq| ≤ 32·127):
+// fp16 (−6144, −hi, −lo, 0, …) with Σq = 64·hi + lo, 0 ≤ lo < 64, so |hi| ≤ 64 — every
+// entry an exact fp16 integer. Against the A row (2048, 64z, z, 0, …) it sums to
+// −(1.5·2^23 + z·Σq).
+__device__ __forceinline__ uint4 conversion_operand(int sum)
+{
+    const int hi = sum >> 6, lo = sum - 64 * hi;
+    return make_uint4(half_bits(-6144) | (half_bits(-hi) << 16), half_bits(-lo), 0u, 0u);
+}
+
+// Byte offset of element group 4·l8..4·l8+3 of (token t, block b) in the code array: half
+// h = (l8 >> 1) & 1 holds elements [8h..8h+7, 16+8h..16+8h+7] of each token.
+__device__ __forceinline__ int64_t act_code_offset(const ActQ8& a, int t, int b, int l8)
+{
+    const int h = (l8 >> 1) & 1;
+    const int idx = 4 * (l8 & 1) + 8 * (l8 >> 2);
+    return ((((int64_t)(t >> 5) * a.B + b) * 2 + h) * 32 + (t & 31)) * 16 + idx;
+}
+
 // One 32-value block: IntegerGemm.QuantizeActivations (semantics 0: d = max|x|/127,
 // q = RNE(x·(1/d)), IntegerGemm.cs:97-138) or IntegerDot.QuantizeActivations (1: q rounded
 // half away from zero and clamped to ±127, d rounded to fp16, IntegerDot.cs:60-98); d and
 // 1/d are IEEE (correctly rounded division is on for this file), d = 0 gives q = 0. Also
-// d·Σq, the offset types' second epilogue factor. The 8 lanes of an aligned lane group
-// (l8 = lane % 8) hold elements 4·l8 .. 4·l8+3; max and Σq are exact in any order, so the
-// group reductions are order-free. Each lane stores its 4 fp16 codes at their permuted
-// positions (8 bytes; the group writes the block's 64-byte row).
+// float(Σq) and d·Σq, the offset types' second epilogue factor. The 8 lanes of an aligned
+// lane group (l8 = lane % 8) hold elements 4·l8 .. 4·l8+3; max and Σq are exact in any
+// order, so the group reductions are order-free. Each lane stores its 4 int8 codes.
 __device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, int t, int b, int semantics)
 {
     float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -141,27 +166,22 @@ __device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, i
     sum += __shfl_xor(sum, 1, 8);
     sum += __shfl_xor(sum, 2, 8);
     sum += __shfl_xor(sum, 4, 8);
-    const uint32_t w0 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q0) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q1) << 16);
-    const uint32_t w1 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q2) |
-                        ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(float)q3) << 16);
-    // element 4·l8 sits at stored position perm⁻¹: groups of 8 keep their order, [8..15] and
-    // [16..23] swap places.
-    const int pos = (l8 == 2 || l8 == 3) ? 4 * l8 + 8 : (l8 == 4 || l8 == 5) ? 4 * l8 - 8 : 4 * l8;
-    uint16_t* row = a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32;
-    *reinterpret_cast<uint2*>(row + pos) = make_uint2(w0, w1);
+    const uint32_t w = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                       ((uint32_t)(q3 & 0xFF) << 24);
+    *reinterpret_cast<uint32_t*>(a.q + act_code_offset(a, t, b, l8)) = w;
     if (l8 == 0) {
         a.d[(int64_t)b * a.Tpad + t] = dd;
+        a.cv[(int64_t)b * a.Tpad + t] = conversion_operand(sum);
         a.ds[(int64_t)b * a.Tpad + t] = dd * (float)sum;
     }
 }
 
 __device__ __forceinline__ void zero_block8(int l8, const ActQ8& a, int t, int b)
 {
-    uint16_t* row = a.q + (((int64_t)(t >> 5) * a.B + b) * 32 + (t & 31)) * 32;
-    *reinterpret_cast<uint2*>(row + 4 * l8) = make_uint2(0u, 0u);
+    *reinterpret_cast<uint32_t*>(a.q + act_code_offset(a, t, b, l8)) = 0u;
     if (l8 == 0) {
         a.d[(int64_t)b * a.Tpad + t] = 0.0f;
+        a.cv[(int64_t)b * a.Tpad + t] = conversion_operand(0);
         a.ds[(int64_t)b * a.Tpad + t] = 0.0f;
     }
 }
@@ -301,205 +321,227 @@ hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& 
 
 // ------------------------------------------------------------------- GEMM
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float v32f __attribute__((ext_vector_type(32)));
-
 // Four 4-bit fifth-bit flags → 0x10 in the byte of each set bit.
 __device__ inline uint32_t expand_bits4(uint32_t x4)
 {
     return ((__umul24(x4, 0x00204081u)) & 0x01010101u) << 4;
 }
 
-// Four weight bytes (each < 256, already offset to be unsigned) → two dwords of fp16
-// 1024 + byte, then minus (1024 + zero point): exact small integers.
-__device__ __forceinline__ void bytes_to_half(uint32_t x, _Float16 bias, uint32_t& lo, uint32_t& hi)
-{
-    const h2 b2 = {bias, bias};
-    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u);
-    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u);
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, p0) + b2);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, p1) + b2);
-}
+template <int TYPE> struct ZeroPoint {
+    static constexpr int z = TYPE == SHS_TYPE_Q4_0 ? 8 : TYPE == SHS_TYPE_Q5_0 ? 16 : 0;  // IntegerGemm.cs:75-81
+};
 
-// Lane half h's MFMA A operands for one 32-wide block of one row: lo = quant elements
-// 8h..8h+7, hi = elements 16+8h..16+8h+7, as fp16 signed weights u − z (u for the
-// offset types). q0/q1 are qs bytes 8h..8h+7 (Q4/Q5) or, for Q8_0, the lane's 16 permuted
-// bytes are q0..q3.
+// Lane half h's 16 weight codes of one row's block as the int8 MFMA's A operand, in the
+// activation order [8h..8h+7, 16+8h..16+8h+7]: the unsigned codes u (nibble, plus the fifth
+// bit for Q5) — their zero point is applied through the activation sums, like the
+// reference's −z·Σa — or the stored signed bytes for Q8_0. q0/q1 are qs bytes 8h..8h+7
+// (Q4/Q5); for Q8_0, q0..q3 are the lane's 16 stored bytes.
 template <int TYPE>
-__device__ __forceinline__ void weights_to_half(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, uint32_t qh, int h,
-                                                v8h& lo, v8h& hi)
+__device__ __forceinline__ v4i weights_i8(uint32_t q0, uint32_t q1, uint32_t q2, uint32_t q3, uint32_t qh, int h)
 {
-    uint32_t e0, e1, e2, e3;  // four dwords of unsigned bytes: elements lo[0..3], lo[4..7], hi[0..3], hi[4..7]
-    _Float16 bias;
-    if (TYPE == SHS_TYPE_Q8_0) {
-        e0 = q0 ^ 0x80808080u; e1 = q1 ^ 0x80808080u; e2 = q2 ^ 0x80808080u; e3 = q3 ^ 0x80808080u;
-        bias = (_Float16)-1152.0f;
-    } else {
-        e0 = q0 & 0x0F0F0F0Fu; e1 = q1 & 0x0F0F0F0Fu;
-        e2 = (q0 >> 4) & 0x0F0F0F0Fu; e3 = (q1 >> 4) & 0x0F0F0F0Fu;
-        if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) {
-            const uint32_t sh = 8u * h;
-            e0 |= expand_bits4((qh >> sh) & 0xFu);
-            e1 |= expand_bits4((qh >> (sh + 4)) & 0xFu);
-            e2 |= expand_bits4((qh >> (sh + 16)) & 0xFu);
-            e3 |= expand_bits4((qh >> (sh + 20)) & 0xFu);
-        }
-        bias = TYPE == SHS_TYPE_Q4_0 ? (_Float16)-1032.0f : TYPE == SHS_TYPE_Q5_0 ? (_Float16)-1040.0f : (_Float16)-1024.0f;
+    if (TYPE == SHS_TYPE_Q8_0) return v4i{(int)q0, (int)q1, (int)q2, (int)q3};
+    uint32_t e0 = q0 & 0x0F0F0F0Fu, e1 = q1 & 0x0F0F0F0Fu;
+    uint32_t e2 = (q0 >> 4) & 0x0F0F0F0Fu, e3 = (q1 >> 4) & 0x0F0F0F0Fu;
+    if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) {
+        const uint32_t sh = 8u * h;
+        e0 |= expand_bits4((qh >> sh) & 0xFu);
+        e1 |= expand_bits4((qh >> (sh + 4)) & 0xFu);
+        e2 |= expand_bits4((qh >> (sh + 16)) & 0xFu);
+        e3 |= expand_bits4((qh >> (sh + 20)) & 0xFu);
     }
-    uint32_t d[8];
-    bytes_to_half(e0, bias, d[0], d[1]);
-    bytes_to_half(e1, bias, d[2], d[3]);
-    bytes_to_half(e2, bias, d[4], d[5]);
-    bytes_to_half(e3, bias, d[6], d[7]);
-    uint4 l4 = make_uint4(d[0], d[1], d[2], d[3]), h4 = make_uint4(d[4], d[5], d[6], d[7]);
-    lo = __builtin_bit_cast(v8h, l4);
-    hi = __builtin_bit_cast(v8h, h4);
+    return v4i{(int)e0, (int)e1, (int)e2, (int)e3};
 }
 
 template <int TYPE>
-__device__ __forceinline__ void load_weight_half(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
-                                                 int64_t rec, int ri, int h, v8h& lo, v8h& hi)
+__device__ __forceinline__ v4i load_weight_i8(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                                              int64_t rec, int ri, int h)
 {
     if (TYPE == SHS_TYPE_Q8_0) {
         const uint4 q = *reinterpret_cast<const uint4*>(wqs + rec * 1024 + ri * 32 + h * 16);
-        weights_to_half<TYPE>(q.x, q.y, q.z, q.w, 0u, h, lo, hi);
-    } else {
-        const uint2 q = *reinterpret_cast<const uint2*>(wqs + rec * 512 + ri * 16 + h * 8);
-        const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
-        weights_to_half<TYPE>(q.x, q.y, 0u, 0u, qh, h, lo, hi);
+        return weights_i8<TYPE>(q.x, q.y, q.z, q.w, 0u, h);
     }
+    const uint2 q = *reinterpret_cast<const uint2*>(wqs + rec * 512 + ri * 16 + h * 8);
+    const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
+    return weights_i8<TYPE>(q.x, q.y, 0u, 0u, qh, h);
 }
 
-// Chunk swizzle of a 64-byte token row in LDS: rows j..j+7 (and j..j+15) map chunk c to
-// distinct 16-byte bank groups.
-__device__ __forceinline__ int row_swz(int row)
+// The integer MFMA accumulates Σu·q onto the bit pattern of 1.5·2^23, which read as fp32 is
+// 1.5·2^23 + Σu·q exactly while |Σu·q| < 2^22 (|Σu·q| ≤ 32·128·127 for every type).
+constexpr int MAGIC_BITS = 0x4B400000;
+
+// The pattern in 16 registers, built once per kernel: the empty asm hides the constant from
+// the compiler, which would otherwise rebuild it before every MFMA that reads it.
+__device__ __forceinline__ v16i magic16()
 {
-    return ((row >> 1) ^ (row >> 3)) & 3;
+    v16i m;
+#pragma unroll
+    for (int r = 0; r < 16; r++) m[r] = MAGIC_BITS;
+    asm volatile("" : "+v"(m));
+    return m;
 }
 
-// The GEMM, by 32-row × 32-token tiles and pairs of quant blocks.
-//  * Integer block sums: two v_mfma_f32_32x32x16_f16 per block on exact fp16 integers
-//    (|w| ≤ 128, |q| ≤ 127, |Σ| < 2^24), so D = float(I_b) exactly.
-//  * Scale tile RN(d_w·d_a) for the two blocks of a pair: one v_mfma_f32_32x32x1_2b_f32
-//    (its block-1 lanes carry the second block), which computes fma(d_w, d_a, 0).
-//  * Epilogue, block by block in order: acc = fma(I_b, S_b, acc) (+ fma(m_w, RN(d_a·Σq),
-//    acc) for the offset types) — IntegerGemm.Multiply4/Multiply1 per output, bit for bit.
-// A block of 4 waves covers 4 row tiles × TT token tiles. The token tiles' activations
-// (fp16, 2 KB per tile and block) are staged in LDS, double-buffered, shared by the waves;
-// each wave streams its own weights. D[i][j] (row i, token j) sits in lane j + 32·(i%8/4),
-// register 4·(i/8) + i%4.
-// Software pipeline, one barrier per pair: the global loads of pair p+1 (activations, raw
-// weight bytes, scales, mins) are issued before pair p's MFMAs and consumed after them —
-// staged into LDS and decoded into the fp16 operand registers — so their latency hides
-// behind pair p's arithmetic.
+// Position of work-group L of `total` in an order where each XCD (work-groups are dealt to
+// the 8 XCDs round-robin) runs one contiguous range of row groups, so its L2 holds its own
+// slice of the weights.
+__device__ __forceinline__ int xcd_order(int L, int total)
+{
+    const int q = total >> 3, r = total & 7, x = L & 7, slot = L >> 3;
+    return x < r ? x * (q + 1) + slot : r * (q + 1) + (x - r) * q + slot;
+}
+
+// ---- asynchronous global → LDS copies (global_load_lds), issued through inline asm so the
+// compiler's own wait insertion (which would wait for every copy before any LDS read) stays
+// out of the pipeline; the kernel waits for them itself with vmcnt. lds is the wave-uniform
+// LDS byte address of the wave's destination: lane i's bytes land at lds + i·size.
+// m0 (the copy's LDS base) is reserved: clang warns about naming it as a clobber; nothing
+// else in these kernels keeps a value in m0 across the copies.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void* g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)p);
+}
+
+// Wait until at most N of this wave's global → LDS copies are outstanding (they complete in
+// order), then meet the work-group at a barrier.
+template <int N>
+__device__ __forceinline__ void wait_copies_barrier()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+// The GEMM y = x·Wᵀ by 32-row × 32-token tiles, block by block in the reference order.
+//  * Integer block sums: one v_mfma_i32_32x32x32_i8 per (tile, block) on the unsigned weight
+//    codes and the int8 activation codes, accumulated onto the magic bit pattern above:
+//    F = 1.5·2^23 + Σu·q as fp32.
+//  * Conversion and zero point: one v_mfma_f32_32x32x16_f16 per (tile, block) with C = F,
+//    A row (2048, 64z, z, 0, …) and the activation's B column (−6144, −⌊Σq/64⌋,
+//    −(Σq mod 64), 0, …): I = F − 1.5·2^23 − z·Σq = Σ(u−z)·q. Every product and partial sum
+//    is an integer below 2^24, so I is exact whatever the MFMA's summation order.
+//  * Scale RN(d_w·d_a): one v_mfma_f32_32x32x1_2b_f32 per two tiles, fma(d_w, d_a, 0).
+//  * Epilogue on the VALU: acc = fma(I_b, S_b, acc) (+ fma(m_w, RN(d_a·Σq), acc) for the
+//    offset types) — IntegerGemm.Multiply4/Multiply1 per output, bit for bit
+//    (IntegerGemm.cs:371-473).
+// The two integer MFMA steps run on the matrix cores beside the VALU epilogue; the fp32
+// scale step and the epilogue share the VALU's issue slots.
+// A work-group is 4 waves, one 32-row tile each, over TT 32-token tiles; the scale step pairs
+// the two token tiles (TT = 2) or two consecutive blocks (TT = 1). The K loop runs over stages
+// of two blocks through a ring of NS LDS slots filled by global → LDS copies NS − 1 stages
+// ahead, so memory latency hides behind NS − 1 stages of arithmetic; one barrier per stage.
+// A slot holds the stage's activation codes and per-token operands (d_a, the conversion
+// column, d_a·Σq; shared by the 4 waves) and each wave's weight bytes and per-row factors
+// (d_w, fifth bits, m_w). D[i][j] (row i, token j) sits in lane j + 32·(i%8/4), register
+// 4·(i/8) + i%4.
+template <int TYPE, int TT>
+struct GemmSlot {
+    static constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
+    static constexpr bool QH = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1);
+    static constexpr bool Q8 = (TYPE == SHS_TYPE_Q8_0);
+    static constexpr int ACT = 2 * TT * 1024;  // [tile][block] 1 KB code chunks
+    // per-token operands: conversion columns [block][TT·32 tokens] 16 B, then d_a and d_a·Σq
+    // [block][TT·32 tokens] f32 (TT = 2: 2 KB + 1 KB; TT = 1: 1 KB + 1 KB incl. padding)
+    static constexpr int CV = 2 * TT * 32 * 16;
+    static constexpr int FACT = CV + 1024;
+    static constexpr int W = Q8 ? 2048 : 1024;               // per wave: [block][32 rows][QSB]
+    static constexpr int WX = 256 * (1 + QH + OFF);          // per wave: d_w [, qh] [, m_w], [block][32 rows]
+    static constexpr int BYTES = ACT + FACT + 4 * (W + WX);
+    static constexpr int NSH_REAL = 2 * TT + CV / 1024 + 1;  // shared 1 KB copies per stage
+    static constexpr int SHARED = (NSH_REAL + 3) / 4;        // per wave (the last wave may repeat one)
+    static constexpr int OWN = (Q8 ? 2 : 1) + 1 + QH + OFF;  // each wave's own copies per stage
+    static constexpr int PER_STAGE = SHARED + OWN;
+    static constexpr int NS = 4;                              // ring depth
+};
+
 template <int TYPE, int TT, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                  const float* __restrict__ wd, const float* __restrict__ wm,
-                                                 int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N)
+                                                 int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N,
+                                                 int n_tg)
 {
-    constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
-    constexpr bool QH = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1);
-    constexpr bool Q8 = (TYPE == SHS_TYPE_Q8_0);
-    constexpr int QW = Q8 ? 4 : 2;       // raw weight dwords per lane and block
-    constexpr int STAGE = TT * 2 * 128;  // uint4 per pair stage: TT tiles × 2 blocks × 2 KB
-    __shared__ uint4 Bs[2][STAGE];
-    __shared__ float Ds[2][2][TT * 32];
-    __shared__ float DSs[2][2][OFF ? TT * 32 : 1];
-    __shared__ float4 Ms[2][4][OFF ? 16 : 1];  // per wave: m of its 32 rows × 2 blocks
+    typedef GemmSlot<TYPE, TT> L;
+    constexpr bool OFF = L::OFF, QH = L::QH, Q8 = L::Q8;
+    constexpr int NS = L::NS;
+    constexpr int Z = ZeroPoint<TYPE>::z;
+    __shared__ __align__(16) uint8_t ring[NS * L::BYTES];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, h = lane >> 5;
-    const int jswz = row_swz(j);
-    const int rt = blockIdx.x * 4 + wave;
+    const int R = xcd_order(blockIdx.x, gridDim.x);
+    const int rg = R / n_tg, tg = R - rg * n_tg;
+    const int rt = rg * 4 + wave;
     const bool active = rt < ntiles;
+    const int rtl = active ? rt : ntiles - 1;  // inactive waves copy a valid tile (their share of the stage)
     const int ntt = a.Tpad >> 5;
-    const int tt0 = blockIdx.y * TT;
-    int nv = ntt - tt0;
-    nv = nv < TT ? nv : TT;
-    const int npairs = (B + 1) >> 1;
-    const uint4* aq = reinterpret_cast<const uint4*>(a.q);
+    const int tt0 = tg * TT;
+    const int nstages = (B + 1) >> 1;
 
-    // ---- raw prefetch registers for one pair
-    uint4 st[TT];             // activation chunks: thread tid owns slots tid + 256k
-    float sd = 0.0f, sds = 0.0f;
-    uint32_t rq[2][QW];       // weight bytes of (row j, lane half h) for blocks 2p, 2p+1
-    uint32_t rqh[2];          // fifth bits of row j, blocks 2p, 2p+1
-    float rdw = 0.0f;         // d_w of (row j, block 2p+h): the scale MFMA's operand
-    float rm = 0.0f;          // m_w of (row j, block 2p+h)
-
-    auto load_raw = [&](int p) {
+    // ---- issue the copies of stage sidx into ring slot `slot`
+    auto issue = [&](int sidx, int slot) {
+        uint8_t* base = ring + slot * L::BYTES;
 #pragma unroll
-        for (int k = 0; k < TT; k++) {
-            const int e = tid + 256 * k;
-            const int u = e >> 8, rem = e & 255, bb = rem >> 7, off = rem & 127;
-            const int blk = 2 * p + bb;
-            st[k] = make_uint4(0, 0, 0, 0);
-            if (u < nv && blk < B) st[k] = aq[((int64_t)(tt0 + u) * B + blk) * 128 + off];
-        }
-        if (tid < 2 * TT * 32) {
-            const int bb = tid / (TT * 32), tok = tid % (TT * 32);
-            const int blk = 2 * p + bb;
-            sd = 0.0f;
-            sds = 0.0f;
-            if ((tok >> 5) < nv && blk < B) {
-                sd = a.d[(int64_t)blk * a.Tpad + tt0 * 32 + tok];
-                if (OFF) sds = a.ds[(int64_t)blk * a.Tpad + tt0 * 32 + tok];
+        for (int k = 0; k < L::SHARED; k++) {
+            int i = wave + 4 * k;
+            if (i >= L::NSH_REAL) i = 0;  // padding: repeat copy 0 (same bytes, same place)
+            if (i < 2 * TT) {
+                // activation codes of (tile u, block bb): 64 lanes × 16 B
+                const int u = i >> 1, bb = i & 1;
+                const int tile = tt0 + u < ntt ? tt0 + u : ntt - 1;
+                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
+                lds_copy16(a.q + ((int64_t)tile * B + blk) * 1024 + lane * 16, lds_addr(base + i * 1024));
+            } else if (i < 2 * TT + L::CV / 1024) {
+                // conversion columns: 64 (block, token) entries of 16 B
+                const int e = (i - 2 * TT) * 64 + lane;  // entry in [block][TT·32]
+                const int bb = e / (TT * 32);
+                int tok = e % (TT * 32);
+                if ((tok >> 5) >= ntt - tt0) tok &= 31;  // a token tile past the end rereads tile tt0
+                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
+                lds_copy16(a.cv + (int64_t)blk * a.Tpad + tt0 * 32 + tok, lds_addr(base + i * 1024));
+            } else {
+                // d_a then d_a·Σq, [block][TT·32] f32 each, 4 floats per lane (lanes past the
+                // arrays repeat d_a)
+                int arr = lane / (TT * 16);
+                int e = (lane % (TT * 16)) * 4;  // float index in [block][TT·32]
+                if (arr > 1 || (arr == 1 && !OFF)) arr = 0;
+                const int bb = e / (TT * 32);
+                int tok = e % (TT * 32);
+                if ((tok >> 5) >= ntt - tt0) tok &= 31;
+                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
+                const float* src = arr == 0 ? a.d : a.ds;
+                lds_copy16(src + (int64_t)blk * a.Tpad + tt0 * 32 + tok, lds_addr(base + i * 1024));
             }
         }
+        // own copies: weight bytes of blocks 2s, 2s+1 (a block past B rereads block B−1)
+        uint8_t* wbase = base + L::ACT + L::FACT + wave * L::W;
+        uint8_t* xbase = base + L::ACT + L::FACT + 4 * L::W + wave * L::WX;
+        if constexpr (Q8) {
 #pragma unroll
-        for (int bb = 0; bb < 2; bb++) {
-            const int blk = 2 * p + bb;
-#pragma unroll
-            for (int w = 0; w < QW; w++) rq[bb][w] = 0u;
-            rqh[bb] = 0u;
-            if (active && blk < B) {
-                const int64_t rec = (int64_t)rt * B + blk;
-                if constexpr (Q8) {
-                    const uint4 q = *reinterpret_cast<const uint4*>(wqs + rec * 1024 + j * 32 + h * 16);
-                    rq[bb][0] = q.x;
-                    rq[bb][1] = q.y;
-                    rq[bb][2] = q.z;
-                    rq[bb][3] = q.w;
-                } else {
-                    const uint2 q = *reinterpret_cast<const uint2*>(wqs + rec * 512 + j * 16 + h * 8);
-                    rq[bb][0] = q.x;
-                    rq[bb][1] = q.y;
-                }
-                if (QH) rqh[bb] = wqh[rec * 32 + j];
+            for (int bb = 0; bb < 2; bb++) {
+                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
+                lds_copy16(wqs + ((int64_t)rtl * B + blk) * 1024 + lane * 16, lds_addr(wbase + bb * 1024));
             }
+        } else {
+            const int blk = 2 * sidx + h < B ? 2 * sidx + h : B - 1;
+            lds_copy16(wqs + ((int64_t)rtl * B + blk) * 512 + j * 16, lds_addr(wbase));
         }
-        const int blk = 2 * p + h;
-        rdw = 0.0f;
-        rm = 0.0f;
-        if (active && blk < B) {
-            rdw = wd[((int64_t)rt * B + blk) * 32 + j];
-            if (OFF) rm = wm[((int64_t)rt * B + blk) * 32 + j];
-        }
-    };
-
-    // ---- operands of the pair being multiplied
-    v8h wlo[2], whi[2];
-    float dw = 0.0f;
-    const int st_slot = (tid & ~3) | ((tid & 3) ^ row_swz((tid & 127) >> 2));
-    auto commit = [&](int buf) {
-#pragma unroll
-        for (int k = 0; k < TT; k++) Bs[buf][st_slot + 256 * k] = st[k];
-        if (tid < 2 * TT * 32) {
-            const int bb = tid / (TT * 32), tok = tid % (TT * 32);
-            Ds[buf][bb][tok] = sd;
-            if (OFF) DSs[buf][bb][tok] = sds;
-        }
-        if (OFF) reinterpret_cast<float*>(Ms[buf][wave])[h * 32 + j] = rm;
-#pragma unroll
-        for (int bb = 0; bb < 2; bb++) {
-            if constexpr (Q8)
-                weights_to_half<TYPE>(rq[bb][0], rq[bb][1], rq[bb][2], rq[bb][3], 0u, h, wlo[bb], whi[bb]);
-            else
-                weights_to_half<TYPE>(rq[bb][0], rq[bb][1], 0u, 0u, rqh[bb], h, wlo[bb], whi[bb]);
-        }
-        dw = rdw;
+        const int blk = 2 * sidx + h < B ? 2 * sidx + h : B - 1;
+        const int64_t rec = ((int64_t)rtl * B + blk) * 32 + j;
+        lds_copy4(wd + rec, lds_addr(xbase));
+        if (QH) lds_copy4(wqh + rec, lds_addr(xbase + 256));
+        if (OFF) lds_copy4(wm + rec, lds_addr(xbase + 256 * (1 + QH)));
     };
 
     v16f acc[TT];
@@ -507,53 +549,115 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
     for (int u = 0; u < TT; u++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[u][r] = 0.0f;
-    const v16f zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     v32f zero32;
 #pragma unroll
     for (int r = 0; r < 32; r++) zero32[r] = 0.0f;
+    const v16i magic = magic16();
+    // A rows of the conversion MFMA: (2048, 64z, z, 0, …) in lane half 0, zeros in half 1
+    v8h acv;
+#pragma unroll
+    for (int k = 0; k < 8; k++) acv[k] = (_Float16)0.0f;
+    if (h == 0) {
+        acv[0] = (_Float16)2048.0f;
+        acv[1] = (_Float16)(float)(64 * Z);
+        acv[2] = (_Float16)(float)Z;
+    }
 
-    load_raw(0);
-    commit(0);
-    __syncthreads();
-    for (int p = 0; p < npairs; ++p) {
-        const int buf = p & 1;
-        const bool more = p + 1 < npairs;
-        if (more) load_raw(p + 1);
-        if (active) {
+    // exact block sums of (token tile u, block bb) from the slot
+    auto block_sums = [&](const uint8_t* base, v4i w, int u, int bb) -> v16f {
+        const v4i q = *reinterpret_cast<const v4i*>(base + (u * 2 + bb) * 1024 + h * 512 + j * 16);
+        const v16i F = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, q, magic, 0, 0, 0);
+        const v8h c = *reinterpret_cast<const v8h*>(base + L::ACT + (bb * TT * 32 + u * 32 + j) * 16);
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(acv, c, __builtin_bit_cast(v16f, F), 0, 0, 0);
+    };
+
+    // m_w·RN(d_a·Σq) of block bb on token tile u (offset types)
+    auto offset_term = [&](const uint8_t* base, int bb, int u, bool valid) {
+        const float* dsa = reinterpret_cast<const float*>(base + L::ACT + L::CV) + 2 * TT * 32;
+        float dsv = dsa[bb * TT * 32 + u * 32 + j];
+        dsv = valid ? dsv : 0.0f;
+        const float4* m4p = reinterpret_cast<const float4*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX +
+                                                            256 * (1 + QH));
 #pragma unroll
-            for (int u = 0; u < TT; u++) {
-                if (u < nv) {
-                    const float da = Ds[buf][h][u * 32 + j];
-                    const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
+        for (int g = 0; g < 4; g++) {
+            const float4 m4 = m4p[bb * 8 + 2 * g + h];
+            acc[u][4 * g] = fmaf(m4.x, dsv, acc[u][4 * g]);
+            acc[u][4 * g + 1] = fmaf(m4.y, dsv, acc[u][4 * g + 1]);
+            acc[u][4 * g + 2] = fmaf(m4.z, dsv, acc[u][4 * g + 2]);
+            acc[u][4 * g + 3] = fmaf(m4.w, dsv, acc[u][4 * g + 3]);
+        }
+    };
+
+    // Weight codes of block bb for lane (row j, half h), from the slot.
+    auto weights = [&](const uint8_t* base, int bb) -> v4i {
+        const uint8_t* wb = base + L::ACT + L::FACT + wave * L::W;
+        if constexpr (Q8) {
+            const uint4 q = *reinterpret_cast<const uint4*>(wb + bb * 1024 + j * 32 + h * 16);
+            return weights_i8<TYPE>(q.x, q.y, q.z, q.w, 0u, h);
+        } else {
+            const uint2 q = *reinterpret_cast<const uint2*>(wb + bb * 512 + j * 16 + h * 8);
+            uint32_t qh = 0u;
+            if (QH)
+                qh = reinterpret_cast<const uint32_t*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX + 256)[bb * 32 + j];
+            return weights_i8<TYPE>(q.x, q.y, 0u, 0u, qh, h);
+        }
+    };
+
+    for (int p = 0; p < NS - 1 && p < nstages; p++) issue(p, p);
+    for (int sidx = 0; sidx < nstages; ++sidx) {
+        // stages issued after this one: NS − 2 in the steady state, fewer at the end
+        const int ahead = nstages - 1 - sidx;
+        if (ahead >= 2) wait_copies_barrier<2 * L::PER_STAGE>();
+        else if (ahead == 1) wait_copies_barrier<L::PER_STAGE>();
+        else wait_copies_barrier<0>();
+        if (sidx + NS - 1 < nstages) issue(sidx + NS - 1, (sidx + NS - 1) % NS);
+        if (!active) continue;
+        const uint8_t* base = ring + (sidx % NS) * L::BYTES;
+        const float* da_s = reinterpret_cast<const float*>(base + L::ACT + L::CV);
+        const float* dw_s = reinterpret_cast<const float*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX);
+        // A block past B (odd B, last stage) holds copies of block B−1: its d_w is taken as 0,
+        // so S = 0 and fma(I, 0, acc) leaves acc unchanged (acc is never −0), and the loop body
+        // needs no branch.
+        const bool valid1 = 2 * sidx + 1 < B;
+        if constexpr (TT == 2) {
 #pragma unroll
-                    for (int bb = 0; bb < 2; bb++) {
-                        const uint4* bp = &Bs[buf][(u * 2 + bb) * 128 + j * 4];
-                        const v8h blo = __builtin_bit_cast(v8h, bp[(2 * h) ^ jswz]);
-                        const v8h bhi = __builtin_bit_cast(v8h, bp[(2 * h + 1) ^ jswz]);
-                        v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(wlo[bb], blo, zero16, 0, 0, 0);
-                        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(whi[bb], bhi, I, 0, 0, 0);
+            for (int bb = 0; bb < 2; bb++) {
+                const bool valid = bb == 0 || valid1;
+                const v4i w = weights(base, bb);
+                const v16f G0 = block_sums(base, w, 0, bb);
+                const v16f G1 = block_sums(base, w, 1, bb);
+                const float da = da_s[bb * 64 + lane];
+                float dw = dw_s[bb * 32 + j];
+                dw = valid ? dw : 0.0f;
+                const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
 #pragma unroll
-                        for (int r = 0; r < 16; r++) acc[u][r] = fmaf(I[r], S[16 * bb + r], acc[u][r]);
-                        if (OFF) {
-                            const float dsv = DSs[buf][bb][u * 32 + j];
-#pragma unroll
-                            for (int g = 0; g < 4; g++) {
-                                const float4 m4 = Ms[buf][wave][bb * 8 + 2 * g + h];
-                                acc[u][4 * g] = fmaf(m4.x, dsv, acc[u][4 * g]);
-                                acc[u][4 * g + 1] = fmaf(m4.y, dsv, acc[u][4 * g + 1]);
-                                acc[u][4 * g + 2] = fmaf(m4.z, dsv, acc[u][4 * g + 2]);
-                                acc[u][4 * g + 3] = fmaf(m4.w, dsv, acc[u][4 * g + 3]);
-                            }
-                        }
-                    }
+                for (int r = 0; r < 16; r++) {
+                    acc[0][r] = fmaf(G0[r], S[r], acc[0][r]);
+                    acc[1][r] = fmaf(G1[r], S[16 + r], acc[1][r]);
+                }
+                if (OFF) {
+                    offset_term(base, bb, 0, valid);
+                    offset_term(base, bb, 1, valid);
                 }
             }
+        } else {
+            const v16f G0 = block_sums(base, weights(base, 0), 0, 0);
+            const v16f G1 = block_sums(base, weights(base, 1), 0, 1);
+            const float da = da_s[h * 32 + j];
+            float dw = dw_s[h * 32 + j];
+            dw = (h == 0 || valid1) ? dw : 0.0f;
+            const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G0[r], S[r], acc[0][r]);
+            if (OFF) offset_term(base, 0, 0, true);
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G1[r], S[16 + r], acc[0][r]);
+            if (OFF) offset_term(base, 1, 0, valid1);
         }
-        if (more) commit(buf ^ 1);
-        __syncthreads();
     }
     if (!active) return;
 
+    const int nv = ntt - tt0 < TT ? ntt - tt0 : TT;
     const bool vec = ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
 #pragma unroll
     for (int u = 0; u < TT; u++) {
@@ -588,8 +692,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
 template <int TYPE, int TT, int MODE>
 static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
 {
-    dim3 grid((unsigned)((w.tiles + 3) / 4), (unsigned)(((a.Tpad >> 5) + TT - 1) / TT)), block(256);
-    hipLaunchKernelGGL((k_gemm<TYPE, TT, MODE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy, w.rows);
+    const int n_rg = (w.tiles + 3) / 4, n_tg = ((a.Tpad >> 5) + TT - 1) / TT;
+    dim3 grid((unsigned)(n_rg * n_tg)), block(256);
+    hipLaunchKernelGGL((k_gemm<TYPE, TT, MODE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy,
+                       w.rows, n_tg);
     return hipGetLastError();
 }
 
@@ -611,32 +717,9 @@ static int gemm_slots()
     return cached[dev];
 }
 
-// Token tiles per block: the largest TT of 4/2/1 whose blocks fill their last round of
-// resident slots to ≥ 90 % (a larger TT decodes each weight block for more tokens, a
-// smaller one has more registers to spare and so more resident blocks).
-template <int TYPE, int MODE>
-static int gemm_tt_of(const DevMatrix& w, const ActQ8& a);
-
-// Token tiles per block: the largest TT of 4/2/1 whose blocks fill their last round of
-// resident slots to ≥ 90 % (a larger TT decodes each weight block for more tokens, a
-// smaller one has more registers to spare and so more resident blocks); between 2 and 1,
-// the better filled, 2 on a tie.
-template <int TYPE, int MODE>
-static hipError_t gemm_mode(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
-{
-    switch (gemm_tt_of<TYPE, MODE>(w, a)) {
-    case 4: return gemm_launch<TYPE, 4, MODE>(w, a, y, ldy, s);
-    case 2: return gemm_launch<TYPE, 2, MODE>(w, a, y, ldy, s);
-    default: return gemm_launch<TYPE, 1, MODE>(w, a, y, ldy, s);
-    }
-}
-
-template <int TYPE>
-static hipError_t gemm_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
-{
-    return mode == GEMM_ADD ? gemm_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s) : gemm_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s);
-}
-
+// Token tiles per work-group: 2 when its work-groups fill their last round of resident
+// slots to ≥ 90 % or at least as well as single tiles would (two tiles decode each weight
+// block once for 64 tokens), else 1.
 template <int TYPE, int MODE>
 static int gemm_tt_of(const DevMatrix& w, const ActQ8& a)
 {
@@ -647,10 +730,23 @@ static int gemm_tt_of(const DevMatrix& w, const ActQ8& a)
         const int64_t rounds = (blocks + slots - 1) / slots;
         return (double)blocks / (double)(rounds * slots);
     };
-    if (ntt >= 4 && fill(4, gemm_slots<TYPE, 4, MODE>()) >= 0.9) return 4;
-    if (ntt >= 2 && fill(2, gemm_slots<TYPE, 2, MODE>()) >= 0.9) return 2;
-    if (ntt >= 2 && fill(2, gemm_slots<TYPE, 2, MODE>()) >= fill(1, gemm_slots<TYPE, 1, MODE>())) return 2;
+    if (ntt < 2) return 1;
+    const double f2 = fill(2, gemm_slots<TYPE, 2, MODE>());
+    if (f2 >= 0.9 || f2 >= fill(1, gemm_slots<TYPE, 1, MODE>())) return 2;
     return 1;
+}
+
+template <int TYPE, int MODE>
+static hipError_t gemm_mode(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+{
+    if (gemm_tt_of<TYPE, MODE>(w, a) == 2) return gemm_launch<TYPE, 2, MODE>(w, a, y, ldy, s);
+    return gemm_launch<TYPE, 1, MODE>(w, a, y, ldy, s);
+}
+
+template <int TYPE>
+static hipError_t gemm_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+{
+    return mode == GEMM_ADD ? gemm_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s) : gemm_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s);
 }
 
 template <int TYPE>
@@ -683,7 +779,8 @@ hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, in
     }
 }
 
-// The MFMA's exact block sums, out[t][r][b] — parity instrumentation.
+// The GEMM's exact block sums, out[t][r][b], through the same two MFMA steps (integer sum
+// onto the magic pattern, then conversion with the zero point) — parity instrumentation.
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_gemm_sums(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                    int ntiles, int B, ActQ8 a, int32_t* __restrict__ out, int N)
@@ -693,19 +790,27 @@ __global__ __launch_bounds__(256) void k_gemm_sums(const uint8_t* __restrict__ w
     const int rt = blockIdx.x * 4 + wave;
     if (rt >= ntiles) return;
     const int tile = blockIdx.y;
-    const v16f zero16 = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const int token = tile * 32 + j;
+    constexpr int Z = ZeroPoint<TYPE>::z;
     const uint4* aq = reinterpret_cast<const uint4*>(a.q);
+    const v16i magic = magic16();
+    v8h acv;
+    for (int k = 0; k < 8; k++) acv[k] = (_Float16)0.0f;
+    if (h == 0) {
+        acv[0] = (_Float16)2048.0f;
+        acv[1] = (_Float16)(float)(64 * Z);
+        acv[2] = (_Float16)(float)Z;
+    }
     for (int b = 0; b < B; ++b) {
-        v8h lo, hi;
-        load_weight_half<TYPE>(wqs, wqh, (int64_t)rt * B + b, j, h, lo, hi);
-        const uint4* bp = aq + ((int64_t)tile * B + b) * 128 + j * 4 + 2 * h;
-        v16f I = __builtin_amdgcn_mfma_f32_32x32x16_f16(lo, __builtin_bit_cast(v8h, bp[0]), zero16, 0, 0, 0);
-        I = __builtin_amdgcn_mfma_f32_32x32x16_f16(hi, __builtin_bit_cast(v8h, bp[1]), I, 0, 0, 0);
+        const v4i w = load_weight_i8<TYPE>(wqs, wqh, (int64_t)rt * B + b, j, h);
+        const v4i q = __builtin_bit_cast(v4i, aq[((int64_t)tile * B + b) * 64 + h * 32 + j]);
+        const v16i F = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, q, magic, 0, 0, 0);
+        const v8h c = __builtin_bit_cast(v8h, a.cv[(int64_t)b * a.Tpad + token]);
+        const v16f G = __builtin_amdgcn_mfma_f32_32x32x16_f16(acv, c, __builtin_bit_cast(v16f, F), 0, 0, 0);
         if (token < a.T)
             for (int r = 0; r < 16; r++) {
                 const int row = rt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (row < N) out[((int64_t)token * N + row) * B + b] = (int32_t)I[r];
+                if (row < N) out[((int64_t)token * N + row) * B + b] = (int32_t)G[r];
             }
     }
 }
@@ -758,16 +863,17 @@ __global__ __launch_bounds__(64) void k_gemv_rows(const uint8_t* __restrict__ wq
     const int ri = r & 31;
     for (int b = threadIdx.x; b < B; b += 64) {
         const int64_t rec = (int64_t)(r >> 5) * B + b;
-        const uint16_t* act = a.q + (((int64_t)(t >> 5) * B + b) * 32 + (t & 31)) * 32;
+        // code position p (half p/16, index p%16) holds element perm_elem(p)
+        const int8_t* act = a.q + (((int64_t)(t >> 5) * B + b) * 2 * 32 + (t & 31)) * 16;
         int I = 0;
         if (TYPE == SHS_TYPE_Q8_0) {
-            const uint8_t* q = wqs + rec * 1024 + ri * 32;  // stored in the activation order
-            for (int p = 0; p < 32; p++) I += (int)(int8_t)q[p] * (int)__builtin_bit_cast(_Float16, act[p]);
+            const uint8_t* q = wqs + rec * 1024 + ri * 32;  // stored in the same element order
+            for (int p = 0; p < 32; p++) I += (int)(int8_t)q[p] * (int)act[(p >> 4) * 512 + (p & 15)];
         } else {
             const uint8_t* q = wqs + rec * 512 + ri * 16;
             const uint32_t qh = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) ? wqh[rec * 32 + ri] : 0u;
             for (int p = 0; p < 32; p++)
-                I += weight_elem<TYPE>(q, qh, perm_elem(p)) * (int)__builtin_bit_cast(_Float16, act[p]);
+                I += weight_elem<TYPE>(q, qh, perm_elem(p)) * (int)act[(p >> 4) * 512 + (p & 15)];
         }
         sI[b] = (float)I;
         sS[b] = wd[rec * 32 + ri] * a.d[(int64_t)b * a.Tpad + t];
