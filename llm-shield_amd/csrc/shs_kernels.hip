@@ -1156,9 +1156,12 @@ __device__ __forceinline__ void attn_scores_work(const AttnChunk ch, int kvh, co
                 nan = nan || sc[r] != sc[r];
             }
         }
-        float4* out = reinterpret_cast<float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
+        // tile layout [query j][residue t][k] for key t + 8k: register r holds key 2r + h,
+        // so residue 2m + h is (sc[m], sc[m+4], sc[m+8], sc[m+12])
+        float* out = scratch + (tile0 + kt) * 1024 + j * 32 + h * 4;
 #pragma unroll
-        for (int g = 0; g < 4; g++) out[g] = make_float4(sc[4 * g], sc[4 * g + 1], sc[4 * g + 2], sc[4 * g + 3]);
+        for (int m = 0; m < 4; m++)
+            *reinterpret_cast<float4*>(out + 8 * m) = make_float4(sc[m], sc[m + 4], sc[m + 8], sc[m + 12]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         nan = nan || __shfl_xor((int)nan, 32);
         if (h == 0) pm[(tile0 + kt) * 32 + j] = nan ? __builtin_nanf("") : mx;
@@ -1195,8 +1198,8 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
     }
     const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);  // Kernels.Softmax: a non-finite max
 
-    // Key t + 8k of a tile sits in lane record j + 32·(t & 1), register (t >> 1) + 4k.
-    const int64_t rec = (int64_t)(j + 32 * (t & 1)) * 16 + (t >> 1);
+    // Keys t + 8k (k = 0..3) of a tile are the float4 at [query j][residue t].
+    const int64_t rec = (int64_t)j * 32 + t * 4;
     auto expo = [&](float sc, int key) {
         return key < nq ? (uniform ? 1.0f : det_expf(sc - mx)) : 0.0f;
     };
@@ -1207,9 +1210,12 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
     auto load = [&](int kt0, float* dst) {
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const float* src = scratch + (tile0 + kt0 + b) * 1024 + rec;
-#pragma unroll
-            for (int k = 0; k < 4; k++) dst[4 * b + k] = kt0 + b < n_kt ? src[4 * k] : 0.0f;
+            const float4 v = kt0 + b < n_kt ? *reinterpret_cast<const float4*>(scratch + (tile0 + kt0 + b) * 1024 + rec)
+                                            : make_float4(0.f, 0.f, 0.f, 0.f);
+            dst[4 * b] = v.x;
+            dst[4 * b + 1] = v.y;
+            dst[4 * b + 2] = v.z;
+            dst[4 * b + 3] = v.w;
         }
     };
     // pass 1: Σe in Kernels.Softmax's order
@@ -1249,9 +1255,10 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (kt0 + b >= n_kt) break;
-            float* dst = scratch + (tile0 + kt0 + b) * 1024 + rec;
-#pragma unroll
-            for (int k = 0; k < 4; k++) dst[4 * k] = expo(sv[4 * b + k], (kt0 + b) * 32 + t + 8 * k) / total;
+            const int key = (kt0 + b) * 32 + t;
+            *reinterpret_cast<float4*>(scratch + (tile0 + kt0 + b) * 1024 + rec) =
+                make_float4(expo(sv[4 * b], key) / total, expo(sv[4 * b + 1], key + 8) / total,
+                            expo(sv[4 * b + 2], key + 16) / total, expo(sv[4 * b + 3], key + 24) / total);
         }
     }
 }
@@ -1285,22 +1292,25 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
     for (int r = 0; r < 16; r++) o[r] = 0.0f;
     // Two tiles in flight: tile kt's weights and V slice load while tile kt − 2 is multiplied.
     struct Stage {
-        float4 w[4];  // this lane's weights (keys 2c + h in register c)
+        float4 w[4];  // this lane's weights: float4 m holds keys 2m + h + 8k, k = 0..3
         float4 v;     // the V slice element this thread stages
     };
+    // weights of query j, key 2c + h: residue 2m + h (m = c & 3), k = c >> 2 of the tile's
+    // [query][residue][k] layout — one float4 per m
     auto load = [&](int kt, Stage& st) {
         st.v = vload(kt);
-        const float4* in = reinterpret_cast<const float4*>(scratch + (tile0 + kt) * 1024 + lane * 16);
+        const float* in = scratch + (tile0 + kt) * 1024 + j * 32 + h * 4;
 #pragma unroll
-        for (int g = 0; g < 4; g++) st.w[g] = active ? in[g] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int m = 0; m < 4; m++)
+            st.w[m] = active ? *reinterpret_cast<const float4*>(in + 8 * m) : make_float4(0.f, 0.f, 0.f, 0.f);
     };
     auto step = [&](int kt, Stage& st) {
         const int buf = kt & 1;
         *reinterpret_cast<float4*>(&Vs[buf][vkey * 32 + vd]) = st.v;
         float w[16];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            w[4 * g] = st.w[g].x; w[4 * g + 1] = st.w[g].y; w[4 * g + 2] = st.w[g].z; w[4 * g + 3] = st.w[g].w;
+        for (int m = 0; m < 4; m++) {
+            w[m] = st.w[m].x; w[m + 4] = st.w[m].y; w[m + 8] = st.w[m].z; w[m + 12] = st.w[m].w;
         }
         __syncthreads();
         if (kt + 2 < n_kt) load(kt + 2, st);
