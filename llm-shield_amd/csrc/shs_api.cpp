@@ -350,6 +350,7 @@ struct shs_model {
     int64_t score_floats = 0, pm_floats = 0;
     int64_t attn_pairs = 0;
     ActBuf act;
+    ActBuf act_ffn;  // the fused gate|up GEMM's output codes (its input codes live in act)
     shs_capture_fn cap_fn = nullptr;
     void* cap_user = nullptr;
     Profiler prof;
@@ -1012,11 +1013,20 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         snprintf(name, sizeof name, "blk.%d.ffn_norm", l);
         if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
 
-        if (run_proj(m, L.gu, ah, gu, 2 * c.ffn, GEMM_STORE, "gemm_gate_up") != SHS_OK) return SHS_E_DEVICE;
         ActQ8 af = a;
         af.K = c.ffn;
         af.B = c.ffn / 32;
-        {
+        if (!cap_on && L.gu.parts.size() == 1) {
+            // one fused matrix: SwiGLU and the down projection's quantization in the epilogue
+            HIP_TRY(m->act_ffn.ensure(T, c.ffn, &af));
+            const DevMatrix& w = L.gu.parts[0];
+            char kname[48] = "k_gemm";
+            if (m->prof.on)
+                snprintf(kname, sizeof kname, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, ah, GEMM_SWIGLU), GEMM_SWIGLU);
+            Timed tm(m->prof, "gemm_gate_up", gemm_ops(T, w), m->stream, kname);
+            HIP_TRY(launch_gemm_swiglu(w, ah, c.ffn / 32, af, m->stream));
+        } else {
+            if (run_proj(m, L.gu, ah, gu, 2 * c.ffn, GEMM_STORE, "gemm_gate_up") != SHS_OK) return SHS_E_DEVICE;
             Timed tm(m->prof, "swiglu_quant", 0, m->stream);
             HIP_TRY(launch_swiglu_quant(gu, 2 * c.ffn, c.ffn, af, nullptr, m->stream));
         }

@@ -59,7 +59,10 @@ struct AttnChunk {
     int item, kt0, nkt, pad;
 };
 
-enum GemmMode { GEMM_STORE = 0, GEMM_ADD = 1 };
+// GEMM_SWIGLU: the fused gate|up matrix (n_ft feature tiles of gate rows, then the same of
+// up rows) with Kernels.SwiGlu and the down projection's 32-block quantization applied in
+// the epilogue; the output is the down projection's activation codes.
+enum GemmMode { GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SWIGLU = 2 };
 
 int qs_bytes(int type);
 bool type_supported(int type);
@@ -73,6 +76,8 @@ hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float e
                                 float* y_opt, hipStream_t s);
 hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& a, float* y_opt, hipStream_t s);
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s);
+// y = SwiGLU(x·[gate|up]ᵀ) quantized into `out` (K = 32·n_ft); w holds 2·n_ft row tiles.
+hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s);
 // The token tiles per block launch_gemm picks for this shape (the k_gemm instantiation's TT).
 int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode);
 hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* out, hipStream_t s);

@@ -464,11 +464,46 @@ struct GemmSlot {
     static constexpr int NS = 4;                              // ring depth
 };
 
+// The down projection's input block (one 32-feature tile × token j) held as the MFMA D
+// layout: lane j + 32h has features 8g + 4h + i in y[4g + i]. Quantized exactly like
+// quant_block8 (semantics 0: d = max|y|/127, q = RNE(y·(1/d))), the max and Σq reduced over
+// the lane pair; codes, d, the conversion column and d·Σq written at token t, block b.
+__device__ __forceinline__ void quant_block_pair(const float* y, int h, const ActQ8& o, int t, int b)
+{
+    float mx = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) mx = fmaxf(mx, fabsf(y[r]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float d = mx / 127.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    int q[16];
+    int sum = 0;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        q[r] = (int)__builtin_rintf(y[r] * inv);
+        sum += q[r];
+    }
+    sum += __shfl_xor(sum, 32);
+    // feature 8g + 4h + i sits in half g & 1 at index 4h + i + 8·(g >> 1)
+    int8_t* base = o.q + (((int64_t)(t >> 5) * o.B + b) * 2 * 32 + (t & 31)) * 16;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const uint32_t w = (uint32_t)(q[4 * g] & 0xFF) | ((uint32_t)(q[4 * g + 1] & 0xFF) << 8) |
+                           ((uint32_t)(q[4 * g + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * g + 3] & 0xFF) << 24);
+        *reinterpret_cast<uint32_t*>(base + (g & 1) * 512 + 4 * h + 8 * (g >> 1)) = w;
+    }
+    if (h == 0) {
+        o.d[(int64_t)b * o.Tpad + t] = d;
+        o.cv[(int64_t)b * o.Tpad + t] = conversion_operand(sum);
+        o.ds[(int64_t)b * o.Tpad + t] = d * (float)sum;
+    }
+}
+
 template <int TYPE, int TT, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                  const float* __restrict__ wd, const float* __restrict__ wm,
                                                  int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N,
-                                                 int n_tg)
+                                                 int n_tg, ActQ8 ao, int n_ft)
 {
     typedef GemmSlot<TYPE, TT> L;
     constexpr bool OFF = L::OFF, QH = L::QH, Q8 = L::Q8;
@@ -482,8 +517,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
     const int j = lane & 31, h = lane >> 5;
     const int R = xcd_order(blockIdx.x, gridDim.x);
     const int rg = R / n_tg, tg = R - rg * n_tg;
-    const int rt = rg * 4 + wave;
-    const bool active = rt < ntiles;
+    // GEMM_SWIGLU: waves 0/1 take gate/up of feature tile 2·rg, waves 2/3 of 2·rg + 1
+    const int ft = 2 * rg + (wave >> 1);
+    const int rt = MODE == GEMM_SWIGLU ? (wave & 1) * n_ft + ft : rg * 4 + wave;
+    const bool active = MODE == GEMM_SWIGLU ? ft < n_ft : rt < ntiles;
     const int rtl = active ? rt : ntiles - 1;  // inactive waves copy a valid tile (their share of the stage)
     const int ntt = a.Tpad >> 5;
     const int tt0 = tg * TT;
@@ -655,9 +692,33 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
             if (OFF) offset_term(base, 1, 0, valid1);
         }
     }
+    const int nv = ntt - tt0 < TT ? ntt - tt0 : TT;
+    if constexpr (MODE == GEMM_SWIGLU) {
+        // Exchange the accumulators through the (now idle) ring: X[wave][u][r][lane]; then
+        // (feature tile 2·rg + p, token tile u) goes to wave 2p + u (waves 0..2·TT−1):
+        // y = sigmoid(g)·(g·u) as Kernels.SwiGlu (Kernels.cs:83-90) forms it, then quantized.
+        float* X = reinterpret_cast<float*>(ring);
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < TT; u++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) X[((wave * TT + u) * 16 + r) * 64 + lane] = acc[u][r];
+        __syncthreads();
+        const int p = wave >> 1, u = wave & 1;
+        const int fti = 2 * rg + p;
+        if (u >= nv || fti >= n_ft) return;
+        float yv[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float g = X[(((2 * p) * TT + u) * 16 + r) * 64 + lane];
+            const float v = X[(((2 * p + 1) * TT + u) * 16 + r) * 64 + lane];
+            yv[r] = (1.0f / (1.0f + det_expf(-g))) * (g * v);
+        }
+        quant_block_pair(yv, h, ao, (tt0 + u) * 32 + j, fti);
+        return;
+    }
     if (!active) return;
 
-    const int nv = ntt - tt0 < TT ? ntt - tt0 : TT;
     const bool vec = ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
 #pragma unroll
     for (int u = 0; u < TT; u++) {
@@ -690,12 +751,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
 }
 
 template <int TYPE, int TT, int MODE>
-static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
+                              const ActQ8& ao = ActQ8(), int n_ft = 0)
 {
-    const int n_rg = (w.tiles + 3) / 4, n_tg = ((a.Tpad >> 5) + TT - 1) / TT;
+    const int n_rg = MODE == GEMM_SWIGLU ? (n_ft + 1) / 2 : (w.tiles + 3) / 4;
+    const int n_tg = ((a.Tpad >> 5) + TT - 1) / TT;
     dim3 grid((unsigned)(n_rg * n_tg)), block(256);
     hipLaunchKernelGGL((k_gemm<TYPE, TT, MODE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy,
-                       w.rows, n_tg);
+                       w.rows, n_tg, ao, n_ft);
     return hipGetLastError();
 }
 
@@ -750,8 +813,16 @@ static hipError_t gemm_type(const DevMatrix& w, const ActQ8& a, float* y, int ld
 }
 
 template <int TYPE>
+static hipError_t gemm_swiglu_type(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& ao, hipStream_t s)
+{
+    if (gemm_tt_of<TYPE, GEMM_SWIGLU>(w, a) == 2) return gemm_launch<TYPE, 2, GEMM_SWIGLU>(w, a, nullptr, 0, s, ao, n_ft);
+    return gemm_launch<TYPE, 1, GEMM_SWIGLU>(w, a, nullptr, 0, s, ao, n_ft);
+}
+
+template <int TYPE>
 static int gemm_tt_type(const DevMatrix& w, const ActQ8& a, int mode)
 {
+    if (mode == GEMM_SWIGLU) return gemm_tt_of<TYPE, GEMM_SWIGLU>(w, a);
     return mode == GEMM_ADD ? gemm_tt_of<TYPE, GEMM_ADD>(w, a) : gemm_tt_of<TYPE, GEMM_STORE>(w, a);
 }
 
@@ -764,6 +835,19 @@ int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode)
     case SHS_TYPE_Q5_1: return gemm_tt_type<SHS_TYPE_Q5_1>(w, a, mode);
     case SHS_TYPE_Q8_0: return gemm_tt_type<SHS_TYPE_Q8_0>(w, a, mode);
     default: return 0;
+    }
+}
+
+hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s)
+{
+    if (w.tiles != 2 * n_ft || out.B != n_ft || out.Tpad != a.Tpad) return hipErrorInvalidValue;
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: return gemm_swiglu_type<SHS_TYPE_Q4_0>(w, a, n_ft, out, s);
+    case SHS_TYPE_Q4_1: return gemm_swiglu_type<SHS_TYPE_Q4_1>(w, a, n_ft, out, s);
+    case SHS_TYPE_Q5_0: return gemm_swiglu_type<SHS_TYPE_Q5_0>(w, a, n_ft, out, s);
+    case SHS_TYPE_Q5_1: return gemm_swiglu_type<SHS_TYPE_Q5_1>(w, a, n_ft, out, s);
+    case SHS_TYPE_Q8_0: return gemm_swiglu_type<SHS_TYPE_Q8_0>(w, a, n_ft, out, s);
+    default: return hipErrorInvalidValue;
     }
 }
 
@@ -1263,11 +1347,17 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
     }
 }
 
+// ctx for NSL consecutive 32-dimension slices (starting at slice NSL·dt) of the 4 query
+// heads of KV head kvh over item idx: one wave per head, the V slices staged in LDS per key
+// tile and shared by the waves; each output is one ordered FMA chain over the keys
+// (Kernels.AddScaled4: ctx = fma(v, w, ctx) in key order), two keys per MFMA step.
+constexpr int ATT_PV_NSL = 2;
 __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const float* __restrict__ vc, int cap,
                                              const AttnItem* __restrict__ items, int n_head, int n_kv,
                                              const float* __restrict__ scratch, float* __restrict__ ctx, int ldc,
-                                             float (*Vs)[32 * 32])
+                                             float (*Vs)[32 * 32 * ATT_PV_NSL])
 {
+    constexpr int NSL = ATT_PV_NSL, DW = 32 * NSL;  // dimensions per work item
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
@@ -1279,26 +1369,27 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
     const int n_kt = att_tiles(it);
     const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + wave) * n_kt;
     const bool qvalid = active && j < it.q_count;
-    const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD + 32 * dt;
+    const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD + DW * dt;
 
-    const int vkey = tid >> 3, vd = 4 * (tid & 7);  // thread tid stages key vkey, dimensions vd .. vd+3
-    auto vload = [&](int kt) {
-        const int kidx = kt * 32 + vkey;
-        return kidx < n_keys ? *reinterpret_cast<const float4*>(vb + (int64_t)kidx * ATT_HD + vd)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-    };
-    v16f o;
+    const int vkey = tid >> 3, vd = 4 * NSL * (tid & 7);  // thread tid stages key vkey, dimensions vd .. vd+4·NSL−1
+    v16f o[NSL];
 #pragma unroll
-    for (int r = 0; r < 16; r++) o[r] = 0.0f;
-    // Two tiles in flight: tile kt's weights and V slice load while tile kt − 2 is multiplied.
+    for (int sl = 0; sl < NSL; sl++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[sl][r] = 0.0f;
+    // Two tiles in flight: tile kt's weights and V slices load while tile kt − 2 is multiplied.
     struct Stage {
-        float4 w[4];  // this lane's weights: float4 m holds keys 2m + h + 8k, k = 0..3
-        float4 v;     // the V slice element this thread stages
+        float4 w[4];    // this lane's weights: float4 m holds keys 2m + h + 8k, k = 0..3
+        float4 v[NSL];  // the V elements this thread stages
     };
     // weights of query j, key 2c + h: residue 2m + h (m = c & 3), k = c >> 2 of the tile's
     // [query][residue][k] layout — one float4 per m
     auto load = [&](int kt, Stage& st) {
-        st.v = vload(kt);
+        const int kidx = kt * 32 + vkey;
+#pragma unroll
+        for (int x = 0; x < NSL; x++)
+            st.v[x] = kidx < n_keys ? *reinterpret_cast<const float4*>(vb + (int64_t)kidx * ATT_HD + vd + 4 * x)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
         const float* in = scratch + (tile0 + kt) * 1024 + j * 32 + h * 4;
 #pragma unroll
         for (int m = 0; m < 4; m++)
@@ -1306,7 +1397,8 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
     };
     auto step = [&](int kt, Stage& st) {
         const int buf = kt & 1;
-        *reinterpret_cast<float4*>(&Vs[buf][vkey * 32 + vd]) = st.v;
+#pragma unroll
+        for (int x = 0; x < NSL; x++) *reinterpret_cast<float4*>(&Vs[buf][vkey * DW + vd + 4 * x]) = st.v[x];
         float w[16];
 #pragma unroll
         for (int m = 0; m < 4; m++) {
@@ -1316,7 +1408,11 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
         if (kt + 2 < n_kt) load(kt + 2, st);
         if (active) {
 #pragma unroll
-            for (int c = 0; c < 16; c++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][(2 * c + h) * 32 + j], w[c], o, 0, 0, 0);
+            for (int c = 0; c < 16; c++)
+#pragma unroll
+                for (int sl = 0; sl < NSL; sl++)
+                    o[sl] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[buf][(2 * c + h) * DW + 32 * sl + j], w[c], o[sl], 0,
+                                                                 0, 0);
         }
     };
     Stage s0, s1;
@@ -1327,10 +1423,13 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
         if (kt + 1 < n_kt) step(kt + 1, s1);
     }
     if (!qvalid) return;
-    float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD + 32 * dt;
+    float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD + DW * dt;
 #pragma unroll
-    for (int g = 0; g < 4; g++)
-        *reinterpret_cast<float4*>(outp + 8 * g + 4 * h) = make_float4(o[4 * g], o[4 * g + 1], o[4 * g + 2], o[4 * g + 3]);
+    for (int sl = 0; sl < NSL; sl++)
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+            *reinterpret_cast<float4*>(outp + 32 * sl + 8 * g + 4 * h) =
+                make_float4(o[sl][4 * g], o[sl][4 * g + 1], o[sl][4 * g + 2], o[sl][4 * g + 3]);
 }
 
 // The work of each attention kernel is handed out longest first from a counter, one item
@@ -1376,12 +1475,13 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, i
                                                  int n_items, int n_head, int n_kv, const float* __restrict__ scratch,
                                                  float* __restrict__ ctx, int ldc, int* __restrict__ counter)
 {
-    __shared__ float Vs[2][32 * 32];  // [key][dimension within the slice]
+    __shared__ float Vs[2][32 * 32 * ATT_PV_NSL];  // [key][dimension within the slices]
     __shared__ int slot;
+    constexpr int NDT = 4 / ATT_PV_NSL;  // work items per (item, KV head)
     for (;;) {
         const int w = next_work(counter, &slot);
-        if (w >= n_items * 4 * n_kv) break;
-        const int per = 4 * n_kv;
+        if (w >= n_items * NDT * n_kv) break;
+        const int per = NDT * n_kv;
         attn_pv_work(n_items - 1 - w / per, (w % per) / n_kv, (w % per) % n_kv, vc, cap, items, n_head, n_kv, scratch,
                      ctx, ldc, Vs);
     }
@@ -1418,7 +1518,7 @@ hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n
                           const float* scratch, float* ctx, int ldc, int* counters, int n_cu, hipStream_t s)
 {
     if (n_items <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_attn_pv, attn_blocks(n_items * 4 * n_kv, 5, n_cu), dim3(256), 0, s, vc, cap, items, n_items,
+    hipLaunchKernelGGL(k_attn_pv, attn_blocks(n_items * (4 / ATT_PV_NSL) * n_kv, 5, n_cu), dim3(256), 0, s, vc, cap, items, n_items,
                        n_head, n_kv, scratch, ctx, ldc, counters + 2);
     return hipGetLastError();
 }
