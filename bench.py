@@ -182,7 +182,7 @@ def main():
     kernels = {}
     for t in TYPE_NAMES:
         for tt in (1, 2, 4):
-            for mode in (0, 1, 2):
+            for mode in (0, 1, 2, 3):
                 name = f"k_gemm<{t},{tt},{mode}>"
                 c, cms, cops = model.profile_read(name)
                 if c:

@@ -949,8 +949,29 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         snprintf(name, sizeof name, "blk.%d.attn_norm", l);
         if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
 
-        if (run_proj(m, L.qkv, ah, qkv, ldqkv, GEMM_STORE, "gemm_qkv") != SHS_OK) return SHS_E_DEVICE;
-        {
+        if (!cap_on && L.qkv.parts.size() == 1 && c.head_dim % 32 == 0) {
+            // one fused matrix: RoPE and the KV-cache store in the epilogue
+            RopeArgs ra;
+            ra.pos = m->pos.as<int32_t>();
+            ra.ct = m->cos_tab.as<float>();
+            ra.st = m->sin_tab.as<float>();
+            ra.qscale = m->qscale_tab.as<float>();
+            ra.half = c.rope_dim / 2;
+            ra.n_head = c.n_head;
+            ra.n_kv = c.n_kv_head;
+            ra.hd = c.head_dim;
+            ra.kc = kc;
+            ra.vc = vc;
+            ra.cap = cap;
+            ra.slot0 = slot0;
+            const DevMatrix& w = L.qkv.parts[0];
+            char kname[48] = "k_gemm";
+            if (m->prof.on)
+                snprintf(kname, sizeof kname, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, ah, GEMM_QKV), GEMM_QKV);
+            Timed tm(m->prof, "gemm_qkv", gemm_ops(T, w), m->stream, kname);
+            HIP_TRY(launch_gemm_qkv(w, ah, qkv, ldqkv, ra, m->stream));
+        } else {
+            if (run_proj(m, L.qkv, ah, qkv, ldqkv, GEMM_STORE, "gemm_qkv") != SHS_OK) return SHS_E_DEVICE;
             Timed tm(m->prof, "rope_store", 0, m->stream);
             HIP_TRY(launch_rope_store(qkv, ldqkv, T, c.n_head, c.n_kv_head, c.head_dim, m->pos.as<int32_t>(),
                                       m->cos_tab.as<float>(), m->sin_tab.as<float>(), m->qscale_tab.as<float>(),

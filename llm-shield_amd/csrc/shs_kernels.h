@@ -62,7 +62,23 @@ struct AttnChunk {
 // GEMM_SWIGLU: the fused gate|up matrix (n_ft feature tiles of gate rows, then the same of
 // up rows) with Kernels.SwiGlu and the down projection's 32-block quantization applied in
 // the epilogue; the output is the down projection's activation codes.
-enum GemmMode { GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SWIGLU = 2 };
+// GEMM_QKV: the fused q|k|v matrix with RoPE (and the query position scale) applied in the
+// epilogue; q goes to the output, k and v to the KV cache (RopeArgs).
+enum GemmMode { GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SWIGLU = 2, GEMM_QKV = 3 };
+
+// RoPE and KV-cache placement for the GEMM_QKV epilogue and k_rope_store: token t sits at
+// position pos[t] and cache slot slot0 + t; tables are [position][half] (cos, sin) and
+// [position] (query scale).
+struct RopeArgs {
+    const int32_t* pos = nullptr;
+    const float* ct = nullptr;
+    const float* st = nullptr;
+    const float* qscale = nullptr;
+    int half = 0, n_head = 0, n_kv = 0, hd = 0;
+    float* kc = nullptr;
+    float* vc = nullptr;
+    int cap = 0, slot0 = 0;
+};
 
 int qs_bytes(int type);
 bool type_supported(int type);
@@ -78,6 +94,8 @@ hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& 
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s);
 // y = SwiGLU(x·[gate|up]ᵀ) quantized into `out` (K = 32·n_ft); w holds 2·n_ft row tiles.
 hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s);
+// q|k|v = x·Wᵀ with RoPE: rotated (and scaled) q into y, rotated k and v into the cache.
+hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s);
 // The token tiles per block launch_gemm picks for this shape (the k_gemm instantiation's TT).
 int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode);
 hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* out, hipStream_t s);

@@ -503,7 +503,7 @@ template <int TYPE, int TT, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                  const float* __restrict__ wd, const float* __restrict__ wm,
                                                  int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N,
-                                                 int n_tg, ActQ8 ao, int n_ft)
+                                                 int n_tg, ActQ8 ao, int n_ft, RopeArgs ra)
 {
     typedef GemmSlot<TYPE, TT> L;
     constexpr bool OFF = L::OFF, QH = L::QH, Q8 = L::Q8;
@@ -718,6 +718,52 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
         return;
     }
     if (!active) return;
+    if constexpr (MODE == GEMM_QKV) {
+        // Rope.Apply on adjacent pairs (x0, x1) → (x0c − x1s, x0s + x1c), unfused, then the
+        // query position scale (MinistralModel.cs:442-482); StoreKeys/StoreValues put k and v
+        // at the token's cache slot. A tile lies inside one head (hd is a multiple of 32).
+        const int hrow = rt * 32 / ra.hd, e0 = rt * 32 % ra.hd;
+#pragma unroll
+        for (int u = 0; u < TT; u++) {
+            const int token = (tt0 + u) * 32 + j;
+            if (u >= nv || token >= a.T) continue;
+            const int p = ra.pos[token];
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int e = e0 + 8 * g + 4 * h;  // element of the head held in acc[u][4g..4g+3]
+                float v[4] = {acc[u][4 * g], acc[u][4 * g + 1], acc[u][4 * g + 2], acc[u][4 * g + 3]};
+                if (hrow < ra.n_head + ra.n_kv) {
+#pragma unroll
+                    for (int k = 0; k < 2; k++) {
+                        const int pi = e / 2 + k;
+                        if (pi < ra.half) {
+                            const float c = ra.ct[(int64_t)p * ra.half + pi], sn = ra.st[(int64_t)p * ra.half + pi];
+                            const float x0 = v[2 * k], x1 = v[2 * k + 1];
+                            const float a0 = x0 * c, b0 = x1 * sn;
+                            const float e1 = x0 * sn, f1 = x1 * c;
+                            v[2 * k] = a0 - b0;
+                            v[2 * k + 1] = e1 + f1;
+                        }
+                    }
+                }
+                float* dst;
+                if (hrow < ra.n_head) {
+                    const float qs = ra.qscale[p];
+                    if (qs != 1.0f) {
+#pragma unroll
+                        for (int k = 0; k < 4; k++) v[k] = v[k] * qs;
+                    }
+                    dst = y + (int64_t)token * ldy + rt * 32 + 8 * g + 4 * h;
+                } else if (hrow < ra.n_head + ra.n_kv) {
+                    dst = ra.kc + ((int64_t)(hrow - ra.n_head) * ra.cap + ra.slot0 + token) * ra.hd + e;
+                } else {
+                    dst = ra.vc + ((int64_t)(hrow - ra.n_head - ra.n_kv) * ra.cap + ra.slot0 + token) * ra.hd + e;
+                }
+                *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+        return;
+    }
 
     const bool vec = ((ldy & 3) == 0) && ((reinterpret_cast<uintptr_t>(y) & 15) == 0);
 #pragma unroll
@@ -752,13 +798,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
 
 template <int TYPE, int TT, int MODE>
 static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
-                              const ActQ8& ao = ActQ8(), int n_ft = 0)
+                              const ActQ8& ao = ActQ8(), int n_ft = 0, const RopeArgs& ra = RopeArgs())
 {
     const int n_rg = MODE == GEMM_SWIGLU ? (n_ft + 1) / 2 : (w.tiles + 3) / 4;
     const int n_tg = ((a.Tpad >> 5) + TT - 1) / TT;
     dim3 grid((unsigned)(n_rg * n_tg)), block(256);
     hipLaunchKernelGGL((k_gemm<TYPE, TT, MODE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy,
-                       w.rows, n_tg, ao, n_ft);
+                       w.rows, n_tg, ao, n_ft, ra);
     return hipGetLastError();
 }
 
@@ -820,8 +866,16 @@ static hipError_t gemm_swiglu_type(const DevMatrix& w, const ActQ8& a, int n_ft,
 }
 
 template <int TYPE>
+static hipError_t gemm_qkv_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s)
+{
+    if (gemm_tt_of<TYPE, GEMM_QKV>(w, a) == 2) return gemm_launch<TYPE, 2, GEMM_QKV>(w, a, y, ldy, s, ActQ8(), 0, ra);
+    return gemm_launch<TYPE, 1, GEMM_QKV>(w, a, y, ldy, s, ActQ8(), 0, ra);
+}
+
+template <int TYPE>
 static int gemm_tt_type(const DevMatrix& w, const ActQ8& a, int mode)
 {
+    if (mode == GEMM_QKV) return gemm_tt_of<TYPE, GEMM_QKV>(w, a);
     if (mode == GEMM_SWIGLU) return gemm_tt_of<TYPE, GEMM_SWIGLU>(w, a);
     return mode == GEMM_ADD ? gemm_tt_of<TYPE, GEMM_ADD>(w, a) : gemm_tt_of<TYPE, GEMM_STORE>(w, a);
 }
@@ -847,6 +901,21 @@ hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, cons
     case SHS_TYPE_Q5_0: return gemm_swiglu_type<SHS_TYPE_Q5_0>(w, a, n_ft, out, s);
     case SHS_TYPE_Q5_1: return gemm_swiglu_type<SHS_TYPE_Q5_1>(w, a, n_ft, out, s);
     case SHS_TYPE_Q8_0: return gemm_swiglu_type<SHS_TYPE_Q8_0>(w, a, n_ft, out, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s)
+{
+    if (ra.hd % 32 != 0 || w.rows != (ra.n_head + 2 * ra.n_kv) * ra.hd || (ldy & 3) != 0 ||
+        (reinterpret_cast<uintptr_t>(y) & 15) != 0)
+        return hipErrorInvalidValue;
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: return gemm_qkv_type<SHS_TYPE_Q4_0>(w, a, y, ldy, ra, s);
+    case SHS_TYPE_Q4_1: return gemm_qkv_type<SHS_TYPE_Q4_1>(w, a, y, ldy, ra, s);
+    case SHS_TYPE_Q5_0: return gemm_qkv_type<SHS_TYPE_Q5_0>(w, a, y, ldy, ra, s);
+    case SHS_TYPE_Q5_1: return gemm_qkv_type<SHS_TYPE_Q5_1>(w, a, y, ldy, ra, s);
+    case SHS_TYPE_Q8_0: return gemm_qkv_type<SHS_TYPE_Q8_0>(w, a, y, ldy, ra, s);
     default: return hipErrorInvalidValue;
     }
 }
