@@ -985,6 +985,9 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             snprintf(name, sizeof name, "blk.%d.v", l);
             if (cp.observe(name, qkv + qdim + kvdim, ldqkv, T, kvdim) != SHS_OK) return SHS_E_DEVICE;
         }
+        ActQ8 ac = a;
+        ac.K = qdim;
+        ac.B = qdim / 32;
         {
             float* scr = m->scores.as<float>();
             float* pm = scr + m->score_floats;
@@ -1001,18 +1004,16 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
                 HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu, m->stream));
             }
             {
+                // without capture, PV writes the o projection's activation codes itself
                 Timed tk(m->prof, "k_attn_pv", attn_ops, m->stream, "attention");
-                HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim, ctr, m->n_cu,
-                                       m->stream));
+                HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim,
+                                       cap_on ? nullptr : &ac, ctr, m->n_cu, m->stream));
             }
         }
         snprintf(name, sizeof name, "blk.%d.attn_weighted", l);
         if (cap_on && cp.observe(name, ctx, qdim, T, qdim) != SHS_OK) return SHS_E_DEVICE;
 
-        ActQ8 ac = a;
-        ac.K = qdim;
-        ac.B = qdim / 32;
-        {
+        if (cap_on) {
             Timed tm(m->prof, "quant_act", 0, m->stream);
             HIP_TRY(launch_quant_act(ctx, qdim, ac, 0, m->stream));
         }

@@ -113,8 +113,11 @@ hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap,
                               float* scratch, float* pm, int* counters, int n_cu, hipStream_t s);
 hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, int n_kv, float* scratch, const float* pm,
                                int* counters, int n_cu, hipStream_t s);
+// ctx, or with `codes` set, ctx quantized per 32-dimension block straight into the o
+// projection's activation codes (rows of items only; ctx is then not written).
 hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
-                          const float* scratch, float* ctx, int ldc, int* counters, int n_cu, hipStream_t s);
+                          const float* scratch, float* ctx, int ldc, const ActQ8* codes, int* counters, int n_cu,
+                          hipStream_t s);
 hipError_t launch_expf(const float* x, int n, float* y, hipStream_t s);
 hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s);
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);

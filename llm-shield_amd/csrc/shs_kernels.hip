@@ -1424,7 +1424,7 @@ constexpr int ATT_PV_NSL = 2;
 __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const float* __restrict__ vc, int cap,
                                              const AttnItem* __restrict__ items, int n_head, int n_kv,
                                              const float* __restrict__ scratch, float* __restrict__ ctx, int ldc,
-                                             float (*Vs)[32 * 32 * ATT_PV_NSL])
+                                             const ActQ8& ao, float (*Vs)[32 * 32 * ATT_PV_NSL])
 {
     constexpr int NSL = ATT_PV_NSL, DW = 32 * NSL;  // dimensions per work item
     const int tid = threadIdx.x;
@@ -1491,6 +1491,22 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
         step(kt, s0);
         if (kt + 1 < n_kt) step(kt + 1, s1);
     }
+    if (ao.q) {
+        // The o projection's quantization of ctx, fused: each slice is one 32-dimension block
+        // of query j, in the layout quant_block_pair takes. Rows past the item's queries are
+        // not written (they belong to the next item, or are padding the GEMM never stores).
+        if (!active) return;
+        const bool valid = j < it.q_count;
+#pragma unroll
+        for (int sl = 0; sl < NSL; sl++) {
+            float y[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) y[r] = o[sl][r];
+            // both lanes of a pair share the query, so they agree on `valid`
+            if (valid) quant_block_pair(y, h, ao, it.q_start + j, (head * ATT_HD + DW * dt + 32 * sl) / 32);
+        }
+        return;
+    }
     if (!qvalid) return;
     float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD + DW * dt;
 #pragma unroll
@@ -1542,7 +1558,7 @@ __global__ __launch_bounds__(256) void k_attn_softmax(const AttnItem* __restrict
 
 __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, int cap, const AttnItem* __restrict__ items,
                                                  int n_items, int n_head, int n_kv, const float* __restrict__ scratch,
-                                                 float* __restrict__ ctx, int ldc, int* __restrict__ counter)
+                                                 float* __restrict__ ctx, int ldc, ActQ8 ao, int* __restrict__ counter)
 {
     __shared__ float Vs[2][32 * 32 * ATT_PV_NSL];  // [key][dimension within the slices]
     __shared__ int slot;
@@ -1552,7 +1568,7 @@ __global__ __launch_bounds__(256) void k_attn_pv(const float* __restrict__ vc, i
         if (w >= n_items * NDT * n_kv) break;
         const int per = NDT * n_kv;
         attn_pv_work(n_items - 1 - w / per, (w % per) / n_kv, (w % per) % n_kv, vc, cap, items, n_head, n_kv, scratch,
-                     ctx, ldc, Vs);
+                     ctx, ldc, ao, Vs);
     }
 }
 
@@ -1584,11 +1600,14 @@ hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, i
 }
 
 hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
-                          const float* scratch, float* ctx, int ldc, int* counters, int n_cu, hipStream_t s)
+                          const float* scratch, float* ctx, int ldc, const ActQ8* codes, int* counters, int n_cu,
+                          hipStream_t s)
 {
     if (n_items <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_attn_pv, attn_blocks(n_items * (4 / ATT_PV_NSL) * n_kv, 5, n_cu), dim3(256), 0, s, vc, cap, items, n_items,
-                       n_head, n_kv, scratch, ctx, ldc, counters + 2);
+    if (codes && (codes->B != n_head * ATT_HD / 32 || !codes->q)) return hipErrorInvalidValue;
+    const ActQ8 ao = codes ? *codes : ActQ8();
+    hipLaunchKernelGGL(k_attn_pv, attn_blocks(n_items * (4 / ATT_PV_NSL) * n_kv, 5, n_cu), dim3(256), 0, s, vc, cap,
+                       items, n_items, n_head, n_kv, scratch, ctx, ldc, ao, counters + 2);
     return hipGetLastError();
 }
 
