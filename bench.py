@@ -30,6 +30,10 @@ TYPE_NAMES = {2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8: "Q8_0"}
 # from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over that kernel, calibrated against a
 # device copy of known size, recorded in profiles/<kernel>_traffic.md.
 COPY_PROBE_BYTES = 256 << 20
+# k_gemm's MODE template argument: what its epilogue does with the accumulators
+EPILOGUES = {0: "store to the output", 1: "add into the residual",
+             2: "SwiGLU of gate|up quantized for the down projection",
+             3: "RoPE on q and k, k and v into the KV cache"}
 
 
 def traffic_file(kernel):
@@ -227,7 +231,7 @@ def main():
                    "tokens": T, "weights": "Q4_0", "seed": args.seed},
         "roofline": {"bound": "mfma",
                      "kernel": f"{roof_kernel}: {TYPE_NAMES[t_]} block-quantized GEMM, {tt_} token tile(s) of 32 per "
-                               f"block, {'add into' if mode_ else 'store to'} the output (int8 ops vs the int8 peak)",
+                               f"block, {EPILOGUES.get(mode_, 'store to the output')} (int8 ops vs the int8 peak)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": read_traffic(roof_kernel, T),
                      "launches": n, "ms_per_launch": round(roof_ms / max(n, 1), 5),
