@@ -83,7 +83,7 @@ struct ActBuf {
         hipError_t e;
         if ((e = q.ensure((size_t)Tpad * K)) != hipSuccess) return e;
         if ((e = d.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
-        if ((e = cv.ensure(sizeof(uint4) * (size_t)Tpad * B)) != hipSuccess) return e;
+        if ((e = cv.ensure(sizeof(uint2) * (size_t)Tpad * B)) != hipSuccess) return e;
         if ((e = ds.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
         view->T = T;
         view->Tpad = Tpad;
@@ -91,7 +91,7 @@ struct ActBuf {
         view->B = B;
         view->q = q.as<int8_t>();
         view->d = d.as<float>();
-        view->cv = cv.as<uint4>();
+        view->cv = cv.as<uint2>();
         view->ds = ds.as<float>();
         return hipSuccess;
     }

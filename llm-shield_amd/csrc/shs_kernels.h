@@ -14,9 +14,9 @@
 //                                          lane half h of the int8 MFMA multiplies, in the order
 //                                          the weight nibbles unpack to
 //     d   [B][Tpad] f32   scale max|x|/127
-//     cv  [B][Tpad] 16 B  the block's conversion operand: fp16 (−6144, −⌊Σq/64⌋, −(Σq mod 64)),
-//                         then zeros — the B column of the fp16 MFMA that turns the integer
-//                         MFMA's offset sums into exact fp32 block sums (see k_gemm)
+//     cv  [B][Tpad] 8 B   the block's conversion operand: fp16 (−6144, −⌊Σq/64⌋, −(Σq mod 64), 0)
+//                         — the B column of the fp16 MFMA that turns the integer MFMA's offset
+//                         sums into exact fp32 block sums (see k_gemm)
 //     ds  [B][Tpad] f32   RN(d·float(Σq)) — the offset types' second factor
 #pragma once
 #include <hip/hip_runtime.h>
@@ -39,7 +39,7 @@ struct ActQ8 {
     int T = 0, Tpad = 0, K = 0, B = 0;
     int8_t* q = nullptr;
     float* d = nullptr;
-    uint4* cv = nullptr;
+    uint2* cv = nullptr;
     float* ds = nullptr;
 };
 

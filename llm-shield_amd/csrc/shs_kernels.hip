@@ -114,13 +114,13 @@ __device__ __forceinline__ uint32_t half_bits(int v)
 }
 
 // The B column of the conversion MFMA for a block with code sum Σq (|Σq| ≤ 32·127):
-// fp16 (−6144, −hi, −lo, 0, …) with Σq = 64·hi + lo, 0 ≤ lo < 64, so |hi| ≤ 64 — every
-// entry an exact fp16 integer. Against the A row (2048, 64z, z, 0, …) it sums to
+// fp16 (−6144, −hi, −lo, 0) with Σq = 64·hi + lo, 0 ≤ lo < 64, so |hi| ≤ 64 — every
+// entry an exact fp16 integer. Against the A row (2048, 64z, z, 0) it sums to
 // −(1.5·2^23 + z·Σq).
-__device__ __forceinline__ uint4 conversion_operand(int sum)
+__device__ __forceinline__ uint2 conversion_operand(int sum)
 {
     const int hi = sum >> 6, lo = sum - 64 * hi;
-    return make_uint4(half_bits(-6144) | (half_bits(-hi) << 16), half_bits(-lo), 0u, 0u);
+    return make_uint2(half_bits(-6144) | (half_bits(-hi) << 16), half_bits(-lo));
 }
 
 // Byte offset of element group 4·l8..4·l8+3 of (token t, block b) in the code array: half
@@ -420,15 +420,15 @@ __device__ __forceinline__ void wait_copies_barrier()
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 // The GEMM y = x·Wᵀ by 32-row × 32-token tiles, block by block in the reference order.
 //  * Integer block sums: one v_mfma_i32_32x32x32_i8 per (tile, block) on the unsigned weight
 //    codes and the int8 activation codes, accumulated onto the magic bit pattern above:
 //    F = 1.5·2^23 + Σu·q as fp32.
-//  * Conversion and zero point: one v_mfma_f32_32x32x16_f16 per (tile, block) with C = F,
-//    A row (2048, 64z, z, 0, …) and the activation's B column (−6144, −⌊Σq/64⌋,
-//    −(Σq mod 64), 0, …): I = F − 1.5·2^23 − z·Σq = Σ(u−z)·q. Every product and partial sum
+//  * Conversion and zero point: one v_mfma_f32_32x32x8_f16 per (tile, block) with C = F,
+//    A row (2048, 64z, z, 0) and the activation's B column (−6144, −⌊Σq/64⌋,
+//    −(Σq mod 64), 0): I = F − 1.5·2^23 − z·Σq = Σ(u−z)·q. Every product and partial sum
 //    is an integer below 2^24, so I is exact whatever the MFMA's summation order.
 //  * Scale RN(d_w·d_a): one v_mfma_f32_32x32x1_2b_f32 per two tiles, fma(d_w, d_a, 0).
 //  * Epilogue on the VALU: acc = fma(I_b, S_b, acc) (+ fma(m_w, RN(d_a·Σq), acc) for the
@@ -452,12 +452,15 @@ struct GemmSlot {
     static constexpr int ACT = 2 * TT * 1024;  // [tile][block] 1 KB code chunks
     // per-token operands: conversion columns [block][TT·32 tokens] 16 B, then d_a and d_a·Σq
     // [block][TT·32 tokens] f32 (TT = 2: 2 KB + 1 KB; TT = 1: 1 KB + 1 KB incl. padding)
-    static constexpr int CV = 2 * TT * 32 * 16;
-    static constexpr int FACT = CV + 1024;
+    // per-token operands, [block][TT·32 tokens] each: conversion columns (8 B), then d_a and
+    // d_a·Σq (4 B) — TT copies of 1 KB
+    static constexpr int CV = 2 * TT * 32 * 8;
+    static constexpr int DA = 2 * TT * 32 * 4;
+    static constexpr int FACT = CV + 2 * DA;
     static constexpr int W = Q8 ? 2048 : 1024;               // per wave: [block][32 rows][QSB]
     static constexpr int WX = 256 * (1 + QH + OFF);          // per wave: d_w [, qh] [, m_w], [block][32 rows]
     static constexpr int BYTES = ACT + FACT + 4 * (W + WX);
-    static constexpr int NSH_REAL = 2 * TT + CV / 1024 + 1;  // shared 1 KB copies per stage
+    static constexpr int NSH_REAL = 2 * TT + FACT / 1024;    // shared 1 KB copies per stage
     static constexpr int SHARED = (NSH_REAL + 3) / 4;        // per wave (the last wave may repeat one)
     static constexpr int OWN = (Q8 ? 2 : 1) + 1 + QH + OFF;  // each wave's own copies per stage
     static constexpr int PER_STAGE = SHARED + OWN;
@@ -539,26 +542,30 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
                 const int tile = tt0 + u < ntt ? tt0 + u : ntt - 1;
                 const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
                 lds_copy16(a.q + ((int64_t)tile * B + blk) * 1024 + lane * 16, lds_addr(base + i * 1024));
-            } else if (i < 2 * TT + L::CV / 1024) {
-                // conversion columns: 64 (block, token) entries of 16 B
-                const int e = (i - 2 * TT) * 64 + lane;  // entry in [block][TT·32]
+            } else {
+                // per-token operands: lane's 16 bytes at FACT offset o — two conversion
+                // columns, or four floats of d_a or d_a·Σq (d_a again when there is no offset
+                // term)
+                const int o = ((i - 2 * TT) * 64 + lane) * 16;
+                const int64_t ld = (int64_t)a.Tpad;
+                const void* src;
+                int e;
+                if (o < L::CV) {
+                    e = o / 8;
+                } else if (o < L::CV + L::DA) {
+                    e = (o - L::CV) / 4;
+                } else {
+                    e = (o - L::CV - L::DA) / 4;
+                }
                 const int bb = e / (TT * 32);
                 int tok = e % (TT * 32);
                 if ((tok >> 5) >= ntt - tt0) tok &= 31;  // a token tile past the end rereads tile tt0
                 const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
-                lds_copy16(a.cv + (int64_t)blk * a.Tpad + tt0 * 32 + tok, lds_addr(base + i * 1024));
-            } else {
-                // d_a then d_a·Σq, [block][TT·32] f32 each, 4 floats per lane (lanes past the
-                // arrays repeat d_a)
-                int arr = lane / (TT * 16);
-                int e = (lane % (TT * 16)) * 4;  // float index in [block][TT·32]
-                if (arr > 1 || (arr == 1 && !OFF)) arr = 0;
-                const int bb = e / (TT * 32);
-                int tok = e % (TT * 32);
-                if ((tok >> 5) >= ntt - tt0) tok &= 31;
-                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
-                const float* src = arr == 0 ? a.d : a.ds;
-                lds_copy16(src + (int64_t)blk * a.Tpad + tt0 * 32 + tok, lds_addr(base + i * 1024));
+                const int64_t idx = blk * ld + tt0 * 32 + tok;
+                if (o < L::CV) src = a.cv + idx;
+                else if (o < L::CV + L::DA || !OFF) src = a.d + idx;
+                else src = a.ds + idx;
+                lds_copy16(src, lds_addr(base + i * 1024));
             }
         }
         // own copies: weight bytes of blocks 2s, 2s+1 (a block past B rereads block B−1)
@@ -590,10 +597,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
 #pragma unroll
     for (int r = 0; r < 32; r++) zero32[r] = 0.0f;
     const v16i magic = magic16();
-    // A rows of the conversion MFMA: (2048, 64z, z, 0, …) in lane half 0, zeros in half 1
-    v8h acv;
+    // A rows of the conversion MFMA: (2048, 64z, z, 0) in lane half 0, zeros in half 1
+    v4h acv;
 #pragma unroll
-    for (int k = 0; k < 8; k++) acv[k] = (_Float16)0.0f;
+    for (int k = 0; k < 4; k++) acv[k] = (_Float16)0.0f;
     if (h == 0) {
         acv[0] = (_Float16)2048.0f;
         acv[1] = (_Float16)(float)(64 * Z);
@@ -604,13 +611,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
     auto block_sums = [&](const uint8_t* base, v4i w, int u, int bb) -> v16f {
         const v4i q = *reinterpret_cast<const v4i*>(base + (u * 2 + bb) * 1024 + h * 512 + j * 16);
         const v16i F = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, q, magic, 0, 0, 0);
-        const v8h c = *reinterpret_cast<const v8h*>(base + L::ACT + (bb * TT * 32 + u * 32 + j) * 16);
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(acv, c, __builtin_bit_cast(v16f, F), 0, 0, 0);
+        const v4h c = *reinterpret_cast<const v4h*>(base + L::ACT + (bb * TT * 32 + u * 32 + j) * 8);
+        return __builtin_amdgcn_mfma_f32_32x32x8f16(acv, c, __builtin_bit_cast(v16f, F), 0, 0, 0);
     };
 
     // m_w·RN(d_a·Σq) of block bb on token tile u (offset types)
     auto offset_term = [&](const uint8_t* base, int bb, int u, bool valid) {
-        const float* dsa = reinterpret_cast<const float*>(base + L::ACT + L::CV) + 2 * TT * 32;
+        const float* dsa = reinterpret_cast<const float*>(base + L::ACT + L::CV + L::DA);
         float dsv = dsa[bb * TT * 32 + u * 32 + j];
         dsv = valid ? dsv : 0.0f;
         const float4* m4p = reinterpret_cast<const float4*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX +
@@ -947,8 +954,8 @@ __global__ __launch_bounds__(256) void k_gemm_sums(const uint8_t* __restrict__ w
     constexpr int Z = ZeroPoint<TYPE>::z;
     const uint4* aq = reinterpret_cast<const uint4*>(a.q);
     const v16i magic = magic16();
-    v8h acv;
-    for (int k = 0; k < 8; k++) acv[k] = (_Float16)0.0f;
+    v4h acv;
+    for (int k = 0; k < 4; k++) acv[k] = (_Float16)0.0f;
     if (h == 0) {
         acv[0] = (_Float16)2048.0f;
         acv[1] = (_Float16)(float)(64 * Z);
@@ -958,8 +965,8 @@ __global__ __launch_bounds__(256) void k_gemm_sums(const uint8_t* __restrict__ w
         const v4i w = load_weight_i8<TYPE>(wqs, wqh, (int64_t)rt * B + b, j, h);
         const v4i q = __builtin_bit_cast(v4i, aq[((int64_t)tile * B + b) * 64 + h * 32 + j]);
         const v16i F = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, q, magic, 0, 0, 0);
-        const v8h c = __builtin_bit_cast(v8h, a.cv[(int64_t)b * a.Tpad + token]);
-        const v16f G = __builtin_amdgcn_mfma_f32_32x32x16_f16(acv, c, __builtin_bit_cast(v16f, F), 0, 0, 0);
+        const v4h c = __builtin_bit_cast(v4h, a.cv[(int64_t)b * a.Tpad + token]);
+        const v16f G = __builtin_amdgcn_mfma_f32_32x32x8f16(acv, c, __builtin_bit_cast(v16f, F), 0, 0, 0);
         if (token < a.T)
             for (int r = 0; r < 16; r++) {
                 const int row = rt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
