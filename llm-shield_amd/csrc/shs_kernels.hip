@@ -236,7 +236,14 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
         return;
     }
     const float* xr = x + (int64_t)t * ldx;
-    for (int i = tid; i < n; i += blockDim.x) sx[i] = xr[i];
+    if (((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (n & 3) == 0) {
+        // float4 row copy, the loads of a thread issued together
+#pragma unroll 4
+        for (int i = tid; i < n / 4; i += blockDim.x)
+            reinterpret_cast<float4*>(sx)[i] = reinterpret_cast<const float4*>(xr)[i];
+    } else {
+        for (int i = tid; i < n; i += blockDim.x) sx[i] = xr[i];
+    }
     __syncthreads();
     if (tid < 16) {
         float acc = 0.0f;
