@@ -1220,7 +1220,7 @@ __device__ __forceinline__ float det_expf(float x)
 //  1. scores: one block per (item, chunk of ≤ 4 key tiles, KV head), a wave per query head;
 //     each 32×32 score tile goes to the scratch with its per-row max;
 //  2. softmax: one block per (item, query head): Σe in order, then w = e / Σe over the scores;
-//  3. values: one block per (item, 32-dimension slice, KV head): the ordered FMA chain of w·v
+//  3. values: one block per (item, 64-dimension half, KV head): the ordered FMA chain of w·v
 //     over the keys.
 // A score tile is stored in the MFMA's D layout with its rows permuted: lane j + 32h,
 // register r holds query j and key 2r + h of the tile (the A operand's row i carries key
@@ -1335,6 +1335,28 @@ __device__ __forceinline__ void attn_scores_work(const AttnChunk ch, int kvh, co
     }
 }
 
+// w = e / Σe, correctly rounded, from rcp = RN(1/Σe): q = RN(e·rcp) is within one ulp of
+// e/Σe, the residual e − q·Σe is exact in one FMA, and RN(q + residual·rcp) is then the
+// correctly rounded quotient (Markstein's theorem) as long as nothing underflows. With
+// 1 ≤ Σe ≤ 2^24 that holds for e ≥ 2^-100 and for e = 0; a lane holding any e in (0, 2^-100)
+// divides outright.
+template <int N>
+__device__ __forceinline__ void softmax_divide(const float* e, float* w, float total, float rcp)
+{
+    bool tiny = false;
+#pragma unroll
+    for (int c = 0; c < N; c++) {
+        tiny = tiny || (__float_as_uint(e[c]) - 1u) < 0x0D7FFFFFu;  // 0 < e < 2^-100
+        const float q = e[c] * rcp;
+        const float r = fmaf(-q, total, e[c]);
+        w[c] = fmaf(r, rcp, q);
+    }
+    if (tiny) {
+#pragma unroll
+        for (int c = 0; c < N; c++) w[c] = e[c] / total;
+    }
+}
+
 // One block per (item, query head); 8 lanes per query row, lane t owning residue t of the
 // row's keys — exactly Kernels.Softmax's Vector<float> lane t, summed in key order.
 __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnItem* __restrict__ items, int n_head,
@@ -1414,18 +1436,23 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
     }
     // pass 2: w = e / Σe over the scores (e recomputed: the exponential is deterministic),
     // written over them; keys outside the row get w = 0
+    const float rcp = 1.0f / total;
     if (qvalid) load(0, nx);
     for (int kt0 = 0; qvalid && kt0 < n_kt; kt0 += NB) {
 #pragma unroll
         for (int i = 0; i < NB * 4; i++) sv[i] = nx[i];
         if (kt0 + NB < n_kt) load(kt0 + NB, nx);
+        float e[NB * 4], w[NB * 4];
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) e[4 * b + k] = expo(sv[4 * b + k], (kt0 + b) * 32 + t + 8 * k);
+        softmax_divide<NB * 4>(e, w, total, rcp);
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             if (kt0 + b >= n_kt) break;
-            const int key = (kt0 + b) * 32 + t;
             *reinterpret_cast<float4*>(scratch + (tile0 + kt0 + b) * 1024 + rec) =
-                make_float4(expo(sv[4 * b], key) / total, expo(sv[4 * b + 1], key + 8) / total,
-                            expo(sv[4 * b + 2], key + 16) / total, expo(sv[4 * b + 3], key + 24) / total);
+                make_float4(w[4 * b], w[4 * b + 1], w[4 * b + 2], w[4 * b + 3]);
         }
     }
 }
