@@ -347,6 +347,8 @@ struct shs_model {
     Buf chunks, counters;  // counters: the attention kernels' three work counters
     int n_chunks = 0;
     int n_cu = 0;          // compute units of the device (persistent kernel sizing)
+    int fused_kt = 0;      // most key tiles an item may have for the fused softmax + values kernel
+    int max_kt = 0;        // key tiles of the longest placed item
     int64_t score_floats = 0, pm_floats = 0;
     int64_t attn_pairs = 0;
     ActBuf act;
@@ -635,6 +637,14 @@ shs_status build_model(const shs_config& c, const SpecMap& tm, int device, int i
     if (e != hipSuccess) return bail(hip_fail(e, "hipStreamCreate"));
     if ((e = hipDeviceGetAttribute(&m->n_cu, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess)
         return bail(hip_fail(e, "hipDeviceGetAttribute"));
+    {
+        // the LDS a block may use once it asks for it (opt-in), else the default limit
+        int optin = 0, base = 0;
+        if ((e = hipDeviceGetAttribute(&optin, hipDeviceAttributeSharedMemPerBlockOptin, device)) != hipSuccess) optin = 0;
+        if ((e = hipDeviceGetAttribute(&base, hipDeviceAttributeMaxSharedMemoryPerBlock, device)) != hipSuccess)
+            return bail(hip_fail(e, "hipDeviceGetAttribute"));
+        m->fused_kt = attn_fused_kt_limit(std::max(optin, base));
+    }
     if ((e = m->counters.ensure(64)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(counters)"));
     m->layers.reserve(c.n_layer);
 
@@ -999,15 +1009,23 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
                 HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(), m->n_chunks,
                                            c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, ctr, m->n_cu, m->stream));
             }
-            {
-                Timed tk(m->prof, "k_attn_softmax", 0, m->stream, "attention");
-                HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu, m->stream));
-            }
-            {
-                // without capture, PV writes the o projection's activation codes itself
-                Timed tk(m->prof, "k_attn_pv", attn_ops, m->stream, "attention");
-                HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim,
-                                       cap_on ? nullptr : &ac, ctr, m->n_cu, m->stream));
+            // without capture, the value step writes the o projection's activation codes itself
+            if (m->max_kt <= m->fused_kt) {
+                // every item's scores fit one block's LDS: softmax and values in one kernel
+                Timed tk(m->prof, "k_attn_softmax_pv", attn_ops, m->stream, "attention");
+                HIP_TRY(launch_attn_softmax_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctx, qdim,
+                                               cap_on ? nullptr : &ac, m->max_kt, m->stream));
+            } else {
+                {
+                    Timed tk(m->prof, "k_attn_softmax", 0, m->stream, "attention");
+                    HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu,
+                                                m->stream));
+                }
+                {
+                    Timed tk(m->prof, "k_attn_pv", attn_ops, m->stream, "attention");
+                    HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim,
+                                           cap_on ? nullptr : &ac, ctr, m->n_cu, m->stream));
+                }
             }
         }
         snprintf(name, sizeof name, "blk.%d.attn_weighted", l);
@@ -1133,6 +1151,8 @@ shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
     }
     m->score_floats = off;
     m->pm_floats = off / 32;
+    m->max_kt = 0;
+    for (const auto& it : items) m->max_kt = std::max(m->max_kt, (it.pos0 + it.q_count + 31) / 32);
     m->attn_pairs = 0;  // (query, key) pairs the items attend over
     for (const auto& it : items) m->attn_pairs += (int64_t)it.q_count * it.pos0 + (int64_t)it.q_count * (it.q_count + 1) / 2;
     HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off + m->pm_floats, 1)));

@@ -118,6 +118,13 @@ hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, i
 hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
                           const float* scratch, float* ctx, int ldc, const ActQ8* codes, int* counters, int n_cu,
                           hipStream_t s);
+// Softmax and values fused (replaces launch_attn_softmax + launch_attn_pv): one block per
+// (item, query head) holds the item's scores in kt_cap LDS tiles; every item must have at
+// most kt_cap key tiles, and kt_cap at most attn_fused_kt_limit(the device's LDS per block).
+hipError_t launch_attn_softmax_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
+                                  const float* scratch, const float* pm, float* ctx, int ldc, const ActQ8* codes,
+                                  int kt_cap, hipStream_t s);
+int attn_fused_kt_limit(int max_lds_bytes);
 hipError_t launch_expf(const float* x, int n, float* y, hipStream_t s);
 hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s);
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);

@@ -1188,11 +1188,11 @@ hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv,
 // 16-bit head of ln 2, the degree-7 Taylor polynomial of e^r in fused Horner form,
 // exact scaling by 2^n), so that any implementation performing the same steps — the
 // CPU restatement included — returns the same bits. ≤ 1 ulp against float64 exp.
+// NaN returns x, x ≤ −104 returns 0 and x above ln(FLT_MAX) returns +inf; those cases
+// are selected after the arithmetic rather than branched around, so a wave whose lanes
+// disagree runs one straight sequence.
 __device__ __forceinline__ float det_expf(float x)
 {
-    if (x != x) return x;
-    if (!(x > -104.0f)) return 0.0f;
-    if (x > 0x1.62e42ep+6f) return INFINITY;
     const float n = __builtin_rintf(x * 0x1.715476p+0f);
     float r = fmaf(-n, 0x1.62e400p-1f, x);
     r = fmaf(-n, 0x1.7f7d1cp-20f, r);
@@ -1204,7 +1204,31 @@ __device__ __forceinline__ float det_expf(float x)
     p = fmaf(p, r, 0x1p-1f);
     p = fmaf(p, r, 0x1p+0f);
     p = fmaf(p, r, 0x1p+0f);
-    return ldexpf(p, (int)n);
+    // n is in [−150, 128] wherever the result is used; the clamp keeps the conversion
+    // defined for the selected-away cases
+    float y = ldexpf(p, (int)fminf(fmaxf(n, -256.0f), 256.0f));
+    y = x > 0x1.62e42ep+6f ? INFINITY : y;
+    y = x > -104.0f ? y : 0.0f;
+    return x != x ? x : y;
+}
+
+// det_expf for x ≤ 0 that is not NaN (a softmax's s − max): the same operations, and the
+// same result, without the tests only a NaN or a positive argument needs.
+__device__ __forceinline__ float det_expf_nonpos(float x)
+{
+    const float n = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = fmaf(-n, 0x1.62e400p-1f, x);
+    r = fmaf(-n, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0x1p-1f);
+    p = fmaf(p, r, 0x1p+0f);
+    p = fmaf(p, r, 0x1p+0f);
+    const float y = ldexpf(p, (int)fmaxf(n, -256.0f));
+    return x > -104.0f ? y : 0.0f;
 }
 
 // Causal GQA attention in MinistralModel.AttendGroup's floating-point order
@@ -1390,7 +1414,8 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
     // Keys t + 8k (k = 0..3) of a tile are the float4 at [query j][residue t].
     const int64_t rec = (int64_t)j * 32 + t * 4;
     auto expo = [&](float sc, int key) {
-        return key < nq ? (uniform ? 1.0f : det_expf(sc - mx)) : 0.0f;
+        const float ex = uniform ? 1.0f : det_expf(sc - mx);
+        return key < nq ? ex : 0.0f;
     };
     float lane_sum = 0.0f, tail_e = 0.0f;
     // Tiles are read in batches of 4 (16 values per lane), the next batch in flight.
@@ -1419,8 +1444,8 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
             for (int k = 0; k < 4; k++) {
                 const int key = (kt0 + b) * 32 + t + 8 * k;
                 const float e = expo(sv[4 * b + k], key);
-                if (key < n8) lane_sum = lane_sum + e;
-                else if (key < nq) tail_e = e;
+                lane_sum = key < n8 ? lane_sum + e : lane_sum;
+                tail_e = key >= n8 && key < nq ? e : tail_e;
             }
     }
     // vsum8: ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)); addition is commutative, so each lane
@@ -1558,6 +1583,185 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
                 make_float4(o[sl][4 * g], o[sl][4 * g + 1], o[sl][4 * g + 2], o[sl][4 * g + 3]);
 }
 
+// Softmax and values of one (item, query head) in one block, the item's scores kept in the
+// LDS between the two: each score is read from memory once, e = exp(s − max) is formed once
+// per element, and the division and the value chains read their operands from the LDS.
+//  * softmax phase: thread (j, t) owns residue t of query row j, as in attn_softmax_work —
+//    Σe in Kernels.Softmax's order, then w = e / Σe over the row's LDS copy;
+//  * value phase: wave w runs the ordered FMA chain of 32-dimension slice w over all keys,
+//    V tiles staged in the LDS (double-buffered) and shared by the four slices.
+// LDS: kt_cap score tiles of 1024 floats, [query j][slot][k] with residue t in slot
+// t ^ (j & 7) (conflict-free float4 writes, 2-way float4 reads), then two V tiles.
+// Blocks map to (KV-head group, head in group) so that the group's heads — which read the
+// same V rows — share an XCD and start together: block b runs group 8·(b >> 5) + (b & 7)
+// (groups longest first) and head (b >> 3) & 3 of it.
+constexpr int ATT_V_TILE = 32 * ATT_HD;  // floats of one staged V tile
+
+__device__ __forceinline__ int att_swz(int j, int t) { return j * 32 + ((t ^ (j & 7)) << 2); }
+
+__global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restrict__ vc, int cap,
+                                                           const AttnItem* __restrict__ items, int n_items,
+                                                           int n_head, int n_kv, const float* __restrict__ scratch,
+                                                           const float* __restrict__ pm, float* __restrict__ ctx,
+                                                           int ldc, ActQ8 ao, int kt_cap)
+{
+    extern __shared__ float4 att_lds4[];
+    float* S = reinterpret_cast<float*>(att_lds4);
+    float* Vs = S + (int64_t)kt_cap * 1024;
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x;
+    const int g = 8 * (b >> 5) + (b & 7), hg = (b >> 3) & 3;
+    const int group = n_head / n_kv;
+    if (g >= n_items * n_kv || hg >= group) return;  // the whole block leaves
+    const int idx = n_items - 1 - g / n_kv, kvh = g % n_kv;
+    const int head = kvh * group + hg;
+    const AttnItem it = items[idx];
+    const int n_kt = att_tiles(it);
+    const int n_keys = it.pos0 + it.q_count;
+    const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + hg) * n_kt;
+
+    // ---- softmax: e over the scores into the LDS, Σe, then w = e / Σe in place
+    {
+        const int j = tid >> 3, t = tid & 7;
+        const bool qvalid = j < it.q_count;
+        const int nq = it.pos0 + j + 1;
+        const int n8 = nq & ~7;
+        float mx = -INFINITY;
+        bool nan = false;
+        for (int kt = t; kt < n_kt; kt += 8) {
+            const float v = pm[(tile0 + kt) * 32 + j];
+            mx = fmaxf(mx, v);
+            nan = nan || v != v;
+        }
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, o, 8));
+            nan = nan || __shfl_xor((int)nan, o, 8);
+        }
+        const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);
+        const int64_t rec = (int64_t)j * 32 + t * 4;
+        const int sw = att_swz(j, t);
+        constexpr int NB = 4;
+        float4 nx[NB], sv[NB];
+        auto load = [&](int kt0) {
+#pragma unroll
+            for (int q = 0; q < NB; q++)
+                nx[q] = kt0 + q < n_kt ? *reinterpret_cast<const float4*>(scratch + (tile0 + kt0 + q) * 1024 + rec)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        };
+        float lane_sum = 0.0f, tail_e = 0.0f;
+        // Tiles below every valid row's n8 — the smallest is row 0's, (pos0 + 1) & ~7, and
+        // pos0 need not be a multiple of 32 — hold only keys each row sees and sums in the
+        // lane order, with s − max ≤ 0 unless the row is uniform: those tiles take a short
+        // path when no valid row of the wave is uniform. Rows past q_count are never read back.
+        const int full_kt = ((it.pos0 + 1) & ~7) >> 5;
+        const bool fast = !__any(qvalid && uniform);
+        if (qvalid) load(0);
+        for (int kt0 = 0; kt0 < n_kt; kt0 += NB) {
+#pragma unroll
+            for (int q = 0; q < NB; q++) sv[q] = nx[q];
+            if (qvalid && kt0 + NB < n_kt) load(kt0 + NB);
+#pragma unroll
+            for (int q = 0; q < NB; q++) {
+                if (kt0 + q >= n_kt) break;
+                const float sc[4] = {sv[q].x, sv[q].y, sv[q].z, sv[q].w};
+                float e[4];
+                if (fast && kt0 + q < full_kt) {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        e[k] = det_expf_nonpos(sc[k] - mx);
+                        lane_sum = lane_sum + e[k];
+                    }
+                    *reinterpret_cast<float4*>(S + (kt0 + q) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
+                    continue;
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    // selects, not branches: the lanes of a row disagree on the key tests
+                    const int key = (kt0 + q) * 32 + t + 8 * k;
+                    const float ex = uniform ? 1.0f : det_expf(sc[k] - mx);
+                    e[k] = qvalid && key < nq ? ex : 0.0f;
+                    lane_sum = key < n8 ? lane_sum + e[k] : lane_sum;
+                    tail_e = key >= n8 && key < nq ? e[k] : tail_e;
+                }
+                *reinterpret_cast<float4*>(S + (kt0 + q) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
+            }
+        }
+        float total = lane_sum + __shfl_xor(lane_sum, 1, 8);
+        total = total + __shfl_xor(total, 2, 8);
+        total = total + __shfl_xor(total, 4, 8);
+#pragma unroll
+        for (int k = 0; k < 7; k++) {
+            const float e = __shfl(tail_e, k, 8);
+            if (n8 + k < nq) total = total + e;
+        }
+        if (qvalid) {
+            const float rcp = 1.0f / total;
+            for (int kt = 0; kt < n_kt; kt++) {
+                float4* p = reinterpret_cast<float4*>(S + kt * 1024 + sw);
+                const float4 v = *p;
+                const float e[4] = {v.x, v.y, v.z, v.w};
+                float w[4];
+                softmax_divide<4>(e, w, total, rcp);
+                *p = make_float4(w[0], w[1], w[2], w[3]);
+            }
+        }
+    }
+
+    // ---- values: slice `wave` of the head
+    const int lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 31, h = lane >> 5;
+    const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD;
+    const int vkey = tid >> 3, vd = 16 * (tid & 7);  // thread tid stages key vkey, dimensions vd .. vd+15
+    float4 vr[4];
+    auto vload = [&](int kt) {
+        const int kidx = kt * 32 + vkey;
+#pragma unroll
+        for (int x = 0; x < 4; x++)
+            vr[x] = kidx < n_keys ? *reinterpret_cast<const float4*>(vb + (int64_t)kidx * ATT_HD + vd + 4 * x)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    v16f o;
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[r] = 0.0f;
+    vload(0);
+    for (int kt = 0; kt < n_kt; kt++) {
+        float* vt = Vs + (kt & 1) * ATT_V_TILE;
+#pragma unroll
+        for (int x = 0; x < 4; x++) *reinterpret_cast<float4*>(vt + vkey * ATT_HD + vd + 4 * x) = vr[x];
+        __syncthreads();  // this V tile staged (and, on the first tile, every w written)
+        if (kt + 1 < n_kt) vload(kt + 1);
+        // weights of query j, key 2c + h: residue 2m + h (m = c & 3), k = c >> 2
+        float w[16];
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float4 v = *reinterpret_cast<const float4*>(S + kt * 1024 + att_swz(j, 2 * m + h));
+            w[m] = v.x;
+            w[m + 4] = v.y;
+            w[m + 8] = v.z;
+            w[m + 12] = v.w;
+        }
+#pragma unroll
+        for (int c = 0; c < 16; c++)
+            o = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[(2 * c + h) * ATT_HD + 32 * wave + j], w[c], o, 0, 0, 0);
+    }
+    if (ao.q) {
+        // the o projection's quantization, as in attn_pv_work
+        if (j < it.q_count) {
+            float y[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) y[r] = o[r];
+            quant_block_pair(y, h, ao, it.q_start + j, (head * ATT_HD + 32 * wave) / 32);
+        }
+        return;
+    }
+    if (j >= it.q_count) return;
+    float* outp = ctx + (int64_t)(it.q_start + j) * ldc + head * ATT_HD + 32 * wave;
+#pragma unroll
+    for (int gq = 0; gq < 4; gq++)
+        *reinterpret_cast<float4*>(outp + 8 * gq + 4 * h) = make_float4(o[4 * gq], o[4 * gq + 1], o[4 * gq + 2], o[4 * gq + 3]);
+}
+
 // The work of each attention kernel is handed out longest first from a counter, one item
 // per block at a time (greedy longest-processing-time order), so that the causal triangle's
 // long rows spread over all CUs whatever the hardware's block placement. Every block leaves
@@ -1649,6 +1853,35 @@ hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n
     const ActQ8 ao = codes ? *codes : ActQ8();
     hipLaunchKernelGGL(k_attn_pv, attn_blocks(n_items * (4 / ATT_PV_NSL) * n_kv, 5, n_cu), dim3(256), 0, s, vc, cap,
                        items, n_items, n_head, n_kv, scratch, ctx, ldc, ao, counters + 2);
+    return hipGetLastError();
+}
+
+int attn_fused_kt_limit(int max_lds_bytes)
+{
+    const int kt = (max_lds_bytes - 2 * ATT_V_TILE * (int)sizeof(float)) / (1024 * (int)sizeof(float));
+    return kt > 0 ? kt : 0;
+}
+
+hipError_t launch_attn_softmax_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
+                                  const float* scratch, const float* pm, float* ctx, int ldc, const ActQ8* codes,
+                                  int kt_cap, hipStream_t s)
+{
+    if (n_items <= 0) return hipSuccess;
+    if (n_head % n_kv != 0 || n_head / n_kv > 4 || kt_cap <= 0) return hipErrorInvalidValue;
+    if (codes && (codes->B != n_head * ATT_HD / 32 || !codes->q)) return hipErrorInvalidValue;
+    const ActQ8 ao = codes ? *codes : ActQ8();
+    const size_t lds = ((size_t)kt_cap * 1024 + 2 * ATT_V_TILE) * sizeof(float);
+    static int attr_set = 0;
+    if (attr_set < (int)lds) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_softmax_pv),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr_set = (int)lds;
+    }
+    const int n_groups = n_items * n_kv;
+    const unsigned grid = (unsigned)(((n_groups + 7) / 8) * 32);
+    hipLaunchKernelGGL(k_attn_softmax_pv, dim3(grid), dim3(256), lds, s, vc, cap, items, n_items, n_head, n_kv, scratch,
+                       pm, ctx, ldc, ao, kt_cap);
     return hipGetLastError();
 }
 

@@ -50,6 +50,34 @@ def test_forward_matches_oracle_and_first_layer_is_bit_exact(shs, oracle, tiny):
     assert np.array_equal(g, o)
 
 
+def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
+    """A pass whose longest 32-query item has at most as many key tiles as one block's LDS
+    holds runs softmax and values fused; a longer one (here 1100 keys, past 1024) takes the
+    three-kernel path. Both are bit-exact, including a pass that starts mid-tile."""
+    cfg, tensors, types, gpu, ora = tiny
+    long_ora = oracle.OracleModel(cfg, tensors, types, cap=1200)
+    rng = np.random.default_rng(11)
+    ids = [1, 200, 511]
+    for prefix, n, fused in ((0, 70, True), (45, 50, True), (0, 1100, False)):
+        toks = rng.integers(0, cfg.vocab, prefix + n)
+        gpu.reset_kv_cache()
+        long_ora.reset()
+        if prefix:
+            gpu.prefill(toks[:prefix])
+            long_ora.forward(toks[:prefix], head_mode=0)
+        gpu.profile(True)
+        gpu.profile_reset()
+        try:
+            g = gpu.forward_selected(toks[prefix:], ids)
+            n_fused = gpu.profile_read("k_attn_softmax_pv")[0]
+            n_split = gpu.profile_read("k_attn_softmax")[0]
+        finally:
+            gpu.profile(False)
+        o = long_ora.forward(toks[prefix:], head_mode=1, vocab_ids=ids)
+        assert np.array_equal(g, o), (prefix, n, H.rel_l2(g, o))
+        assert (n_fused, n_split) == ((cfg.n_layer, 0) if fused else (0, cfg.n_layer)), (prefix, n)
+
+
 def test_selected_rows_are_bit_identical_to_the_full_head(shs, tiny):
     """SystemPromptCacheTests.ScoringReadsExactlyWhatTheFullHeadWouldHave."""
     cfg, tensors, types, gpu, ora = tiny
