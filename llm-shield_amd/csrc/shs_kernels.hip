@@ -15,6 +15,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 int qs_bytes(int type) { return type == SHS_TYPE_Q8_0 ? 32 : 16; }
 bool type_supported(int t) { return t == 2 || t == 3 || t == 6 || t == 7 || t == 8; }
@@ -1713,37 +1714,83 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
     const int j = lane & 31, h = lane >> 5;
     const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD;
     const int vkey = tid >> 3, vd = 16 * (tid & 7);  // thread tid stages key vkey, dimensions vd .. vd+15
-    float4 vr[4];
-    auto vload = [&](int kt) {
+    // Software-pipelined over the key tiles. After the barrier of iteration kt, tile kt + 1's
+    // V sits in LDS buffer (kt + 1) & 1 and every wave is done reading buffer kt & 1 (tile
+    // kt's operands were read in iteration kt − 1). Iteration kt then writes V(kt + 2) into
+    // buffer kt & 1, starts the global load of V(kt + 4), reads tile kt + 1's MFMA operands,
+    // and issues tile kt's 16 MFMAs — the memory instructions interleaved between them, so
+    // they go out while the matrix pipe is busy, and the barrier never waits on fresh LDS
+    // writes. The body has no branch: past the last tile its stores and reads touch
+    // buffers nobody reads again (all inside the block's LDS), and V rows are clamped.
+    struct VRows {
+        v4f v[4];  // native vectors: a float4 struct copy would go through private memory
+    };
+    struct TileOps {
+        float w[16];  // weights of query j, key 2c + h
+        float a[16];  // V of key 2c + h, dimension 32·wave + j
+    };
+    // Rows past the item's last key (and tiles past the last) read that key's row again:
+    // their weights are exactly 0, so fma(v, 0, ctx) leaves ctx as it is — as for the
+    // in-range keys a query does not see — and the loads carry no branch.
+    auto vload = [&](int kt, VRows& r) {
         const int kidx = kt * 32 + vkey;
+        const float* src = vb + (int64_t)(kidx < n_keys ? kidx : n_keys - 1) * ATT_HD + vd;
 #pragma unroll
-        for (int x = 0; x < 4; x++)
-            vr[x] = kidx < n_keys ? *reinterpret_cast<const float4*>(vb + (int64_t)kidx * ATT_HD + vd + 4 * x)
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int x = 0; x < 4; x++) r.v[x] = *reinterpret_cast<const v4f*>(src + 4 * x);
+    };
+    auto vstore = [&](int kt, const VRows& r) {
+        float* vt = Vs + (kt & 1) * ATT_V_TILE;
+#pragma unroll
+        for (int x = 0; x < 4; x++) *reinterpret_cast<v4f*>(vt + vkey * ATT_HD + vd + 4 * x) = r.v[x];
+    };
+    auto oread = [&](int kt, TileOps& op) {
+        // weights: residue 2m + h (m = c & 3), k = c >> 2 of the tile's rows; tile kt_cap
+        // (past the last) reads the first V buffer instead, unused
+        const float* st = S + (kt < kt_cap ? kt : 0) * 1024;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const float4 v = *reinterpret_cast<const float4*>(st + att_swz(j, 2 * m + h));
+            op.w[m] = v.x;
+            op.w[m + 4] = v.y;
+            op.w[m + 8] = v.z;
+            op.w[m + 12] = v.w;
+        }
+        const float* vt = Vs + (kt & 1) * ATT_V_TILE;
+#pragma unroll
+        for (int c = 0; c < 16; c++) op.a[c] = vt[(2 * c + h) * ATT_HD + 32 * wave + j];
     };
     v16f o;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] = 0.0f;
-    vload(0);
-    for (int kt = 0; kt < n_kt; kt++) {
-        float* vt = Vs + (kt & 1) * ATT_V_TILE;
+    VRows ra, rb;
+    TileOps oa, ob;
+    vload(0, ra);
+    vload(1, rb);
+    vstore(0, ra);
+    vstore(1, rb);
+    vload(2, ra);
+    vload(3, rb);
+    __syncthreads();  // V(0), V(1) staged, and every w written
+    oread(0, oa);
+    // iteration kt: `vs` holds V(kt + 2), `cur` tile kt's operands
+    auto step = [&](int kt, VRows& vs, TileOps& cur, TileOps& nxt) {
+        __syncthreads();
+        vstore(kt + 2, vs);
+        vload(kt + 4, vs);
+        oread(kt + 1, nxt);
 #pragma unroll
-        for (int x = 0; x < 4; x++) *reinterpret_cast<float4*>(vt + vkey * ATT_HD + vd + 4 * x) = vr[x];
-        __syncthreads();  // this V tile staged (and, on the first tile, every w written)
-        if (kt + 1 < n_kt) vload(kt + 1);
-        // weights of query j, key 2c + h: residue 2m + h (m = c & 3), k = c >> 2
-        float w[16];
+        for (int c = 0; c < 16; c++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[c], cur.w[c], o, 0, 0, 0);
+        // one memory instruction after each MFMA (LDS write, global load, LDS read)
+        __builtin_amdgcn_sched_group_barrier(0x0200, 4, 0);
 #pragma unroll
-        for (int m = 0; m < 4; m++) {
-            const float4 v = *reinterpret_cast<const float4*>(S + kt * 1024 + att_swz(j, 2 * m + h));
-            w[m] = v.x;
-            w[m + 4] = v.y;
-            w[m + 8] = v.z;
-            w[m + 12] = v.w;
+        for (int c = 0; c < 16; c++) {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0020 | 0x0100, 1, 0);
         }
-#pragma unroll
-        for (int c = 0; c < 16; c++)
-            o = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[(2 * c + h) * ATT_HD + 32 * wave + j], w[c], o, 0, 0, 0);
+    };
+    for (int kt = 0; kt < n_kt; kt += 2) {
+        step(kt, ra, oa, ob);
+        if (kt + 1 < n_kt) step(kt + 1, rb, ob, oa);
     }
     if (ao.q) {
         // the o projection's quantization, as in attn_pv_work
