@@ -1642,7 +1642,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
         const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);
         const int64_t rec = (int64_t)j * 32 + t * 4;
         const int sw = att_swz(j, t);
-        constexpr int NB = 4;
+        constexpr int NB = 8;  // tiles in flight per thread: one block per CU hides no latency
         float4 nx[NB], sv[NB];
         auto load = [&](int kt0) {
 #pragma unroll
@@ -1697,14 +1697,25 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
             if (n8 + k < nq) total = total + e;
         }
         if (qvalid) {
+            // four tiles per round, their reads issued together
             const float rcp = 1.0f / total;
-            for (int kt = 0; kt < n_kt; kt++) {
-                float4* p = reinterpret_cast<float4*>(S + kt * 1024 + sw);
-                const float4 v = *p;
-                const float e[4] = {v.x, v.y, v.z, v.w};
-                float w[4];
-                softmax_divide<4>(e, w, total, rcp);
-                *p = make_float4(w[0], w[1], w[2], w[3]);
+            for (int kt0 = 0; kt0 < n_kt; kt0 += 4) {
+                float e[16], w[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int kt = kt0 + q < n_kt ? kt0 + q : kt0;  // past the end: reread, not written
+                    const float4 v = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
+                    e[4 * q] = v.x;
+                    e[4 * q + 1] = v.y;
+                    e[4 * q + 2] = v.z;
+                    e[4 * q + 3] = v.w;
+                }
+                softmax_divide<16>(e, w, total, rcp);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (kt0 + q < n_kt)
+                        *reinterpret_cast<float4*>(S + (kt0 + q) * 1024 + sw) =
+                            make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
             }
         }
     }
@@ -1788,10 +1799,14 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
             __builtin_amdgcn_sched_group_barrier(0x0020 | 0x0100, 1, 0);
         }
     };
-    for (int kt = 0; kt < n_kt; kt += 2) {
+    // whole pairs, then the odd tile: every path into the loop head carries the same
+    // outstanding loads (V(kt + 2), then V(kt + 3)), so each store waits for its own alone
+    int kt = 0;
+    for (; kt + 1 < n_kt; kt += 2) {
         step(kt, ra, oa, ob);
-        if (kt + 1 < n_kt) step(kt + 1, rb, ob, oa);
+        step(kt + 1, rb, ob, oa);
     }
+    if (kt < n_kt) step(kt, ra, oa, ob);
     if (ao.q) {
         // the o projection's quantization, as in attn_pv_work
         if (j < it.q_count) {
