@@ -1262,7 +1262,8 @@ constexpr int ATT_KROW = ATT_HD + 4;
 __device__ __forceinline__ void attn_scores_work(const AttnChunk ch, int kvh, const float* __restrict__ q, int ldq,
                                                  const float* __restrict__ kc, int cap,
                                                  const AttnItem* __restrict__ items, int n_head, int n_kv, float scale,
-                                                 float* __restrict__ scratch, float* __restrict__ pm, float* Ks)
+                                                 float* __restrict__ scratch, float* __restrict__ pm,
+                                                 float (*Ks)[32 * ATT_KROW])
 {
     constexpr int KROW = ATT_KROW;
     const int tid = threadIdx.x;
@@ -1290,7 +1291,6 @@ __device__ __forceinline__ void attn_scores_work(const AttnChunk ch, int kvh, co
     }
     // A operands: row i of the A tile carries key kap(i), so D row i holds key kap(i).
     const int kap = 8 * (j >> 3) + 2 * (j & 3) + ((j >> 2) & 1);
-    const float* krow = Ks + kap * KROW + 8 * h;
 
     float4 kr[4];  // next K tile: thread tid holds key e >> 5, elements 4(e & 31) .. +3 for e = tid + 256i
     auto kload = [&](int kt) {
@@ -1302,61 +1302,75 @@ __device__ __forceinline__ void attn_scores_work(const AttnChunk ch, int kvh, co
                                   : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
-    kload(ch.kt0);
-    for (int u = 0; u < ch.nkt; ++u) {
-        const int kt = ch.kt0 + u;
-        __syncthreads();
+    auto kstore = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = tid + 256 * i;
-            *reinterpret_cast<float4*>(&Ks[(e >> 5) * KROW + 4 * (e & 31)]) = kr[i];
+            *reinterpret_cast<float4*>(&Ks[buf][(e >> 5) * KROW + 4 * (e & 31)]) = kr[i];
         }
-        __syncthreads();
-        if (u + 1 < ch.nkt) kload(kt + 1);
-        if (!active) continue;
-        // The 8 chains advance together: step s is 8 independent MFMAs.
+    };
+    // K tiles double-buffered, one barrier per tile: tile u + 1 is written into the other
+    // buffer after tile u's MFMAs (its last readers, tile u − 1, finished before the previous
+    // barrier), and its global load was issued a tile earlier.
+    kload(ch.kt0);
+    kstore(0);
+    if (ch.nkt > 1) kload(ch.kt0 + 1);
+    __syncthreads();
+    for (int u = 0; u < ch.nkt; ++u) {
+        const int kt = ch.kt0 + u;
+        const float* krow = Ks[u & 1] + kap * KROW + 8 * h;
         v16f c[8];
+        if (active) {
+            // The 8 chains advance together: step s is 8 independent MFMAs.
 #pragma unroll
-        for (int l = 0; l < 8; l++)
+            for (int l = 0; l < 8; l++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) c[l][r] = 0.0f;
+                for (int r = 0; r < 16; r++) c[l][r] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const float4 k0 = *reinterpret_cast<const float4*>(krow + 16 * s);
-            const float4 k1 = *reinterpret_cast<const float4*>(krow + 16 * s + 4);
-            c[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.x, qv[s][0].x, c[0], 0, 0, 0);
-            c[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.y, qv[s][0].y, c[1], 0, 0, 0);
-            c[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.z, qv[s][0].z, c[2], 0, 0, 0);
-            c[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.w, qv[s][0].w, c[3], 0, 0, 0);
-            c[4] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.x, qv[s][1].x, c[4], 0, 0, 0);
-            c[5] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.y, qv[s][1].y, c[5], 0, 0, 0);
-            c[6] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.z, qv[s][1].z, c[6], 0, 0, 0);
-            c[7] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.w, qv[s][1].w, c[7], 0, 0, 0);
-        }
-        float sc[16];
-        float mx = -INFINITY;
-        bool nan = false;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            // vsum8 of the chains, then the scale
-            const float a = (c[0][r] + c[1][r]) + (c[2][r] + c[3][r]);
-            const float b = (c[4][r] + c[5][r]) + (c[6][r] + c[7][r]);
-            sc[r] = (a + b) * scale;
-            const int key = kt * 32 + 2 * r + h;
-            if (qvalid && key < nq) {
-                mx = fmaxf(mx, sc[r]);
-                nan = nan || sc[r] != sc[r];
+            for (int s = 0; s < 8; s++) {
+                const float4 k0 = *reinterpret_cast<const float4*>(krow + 16 * s);
+                const float4 k1 = *reinterpret_cast<const float4*>(krow + 16 * s + 4);
+                c[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.x, qv[s][0].x, c[0], 0, 0, 0);
+                c[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.y, qv[s][0].y, c[1], 0, 0, 0);
+                c[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.z, qv[s][0].z, c[2], 0, 0, 0);
+                c[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.w, qv[s][0].w, c[3], 0, 0, 0);
+                c[4] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.x, qv[s][1].x, c[4], 0, 0, 0);
+                c[5] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.y, qv[s][1].y, c[5], 0, 0, 0);
+                c[6] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.z, qv[s][1].z, c[6], 0, 0, 0);
+                c[7] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.w, qv[s][1].w, c[7], 0, 0, 0);
             }
         }
-        // tile layout [query j][residue t][k] for key t + 8k: register r holds key 2r + h,
-        // so residue 2m + h is (sc[m], sc[m+4], sc[m+8], sc[m+12])
-        float* out = scratch + (tile0 + kt) * 1024 + j * 32 + h * 4;
+        if (u + 1 < ch.nkt) kstore((u + 1) & 1);
+        if (u + 2 < ch.nkt) kload(kt + 2);
+        if (active) {
+            float sc[16];
+            float mx = -INFINITY;
+            bool nan = false;
+            // A tile below every row's first masked key (pos0 + 1) needs no mask: rows past
+            // q_count are never read back, whatever their maximum.
+            const bool full = (kt + 1) * 32 <= it.pos0 + 1;
 #pragma unroll
-        for (int m = 0; m < 4; m++)
-            *reinterpret_cast<float4*>(out + 8 * m) = make_float4(sc[m], sc[m + 4], sc[m + 8], sc[m + 12]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        nan = nan || __shfl_xor((int)nan, 32);
-        if (h == 0) pm[(tile0 + kt) * 32 + j] = nan ? __builtin_nanf("") : mx;
+            for (int r = 0; r < 16; r++) {
+                // vsum8 of the chains, then the scale
+                const float a = (c[0][r] + c[1][r]) + (c[2][r] + c[3][r]);
+                const float b = (c[4][r] + c[5][r]) + (c[6][r] + c[7][r]);
+                sc[r] = (a + b) * scale;
+                const int key = kt * 32 + 2 * r + h;
+                const bool valid = full || (qvalid && key < nq);  // selects, not branches
+                mx = valid ? fmaxf(mx, sc[r]) : mx;
+                nan = nan || (valid && sc[r] != sc[r]);
+            }
+            // tile layout [query j][residue t][k] for key t + 8k: register r holds key 2r + h,
+            // so residue 2m + h is (sc[m], sc[m+4], sc[m+8], sc[m+12])
+            float* out = scratch + (tile0 + kt) * 1024 + j * 32 + h * 4;
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                *reinterpret_cast<float4*>(out + 8 * m) = make_float4(sc[m], sc[m + 4], sc[m + 8], sc[m + 12]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            nan = nan || __shfl_xor((int)nan, 32);
+            if (h == 0) pm[(tile0 + kt) * 32 + j] = nan ? __builtin_nanf("") : mx;
+        }
+        __syncthreads();
     }
 }
 
@@ -1842,13 +1856,11 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(const float* __restrict_
                                                         int n_kv, float scale, float* __restrict__ scratch,
                                                         float* __restrict__ pm, int* __restrict__ counter)
 {
-    __shared__ float Ks[32 * ATT_KROW];
-    __shared__ int slot;
-    for (;;) {
-        const int w = next_work(counter, &slot);
-        if (w >= n_chunks * n_kv) break;
-        attn_scores_work(chunks[w / n_kv], w % n_kv, q, ldq, kc, cap, items, n_head, n_kv, scale, scratch, pm, Ks);
-    }
+    // one block per (chunk, KV head); the chunks come longest first, and the hardware hands
+    // out blocks in order, so the causal triangle's long rows start first
+    __shared__ float Ks[2][32 * ATT_KROW];
+    const int w = blockIdx.x;
+    attn_scores_work(chunks[w / n_kv], w % n_kv, q, ldq, kc, cap, items, n_head, n_kv, scale, scratch, pm, Ks);
 }
 
 __global__ __launch_bounds__(256) void k_attn_softmax(const AttnItem* __restrict__ items, int n_items, int n_head,
@@ -1892,7 +1904,7 @@ hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap,
     if (n_chunks <= 0) return hipSuccess;
     hipError_t e = launch_fill_zero(reinterpret_cast<float*>(counters), 3, s);  // the three work counters
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k_attn_scores, attn_blocks(n_chunks * n_kv, 2, n_cu), dim3(256), 0, s, q, ldq, kc, cap, items,
+    hipLaunchKernelGGL(k_attn_scores, dim3((unsigned)(n_chunks * n_kv)), dim3(256), 0, s, q, ldq, kc, cap, items,
                        chunks, n_chunks, n_head, n_kv, scale, scratch, pm, counters);
     return hipGetLastError();
 }
