@@ -1007,7 +1007,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             {
                 Timed tk(m->prof, "k_attn_scores", attn_ops, m->stream, "attention");
                 HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(), m->n_chunks,
-                                           c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, ctr, m->n_cu, m->stream));
+                                           c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, m->stream));
             }
             // without capture, the value step writes the o projection's activation codes itself
             if (m->max_kt <= m->fused_kt) {

@@ -106,11 +106,12 @@ hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv_
                              const int32_t* pos, const float* cos_tab, const float* sin_tab,
                              const float* qscale_tab, int half, float* kc, float* vc, int cap,
                              int kv_slot0, hipStream_t s);
-// Causal GQA attention in three launches on one stream (scores, softmax, values); the
-// first clears the three work counters (counters[0..2]) the launches share.
+// Causal GQA attention: the scores, then either the fused softmax + values kernel or the
+// softmax and values launches; the softmax launch clears the two work counters
+// (counters[0..1]) it and the values launch share.
 hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap, const AttnItem* items,
                               const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim, float scale,
-                              float* scratch, float* pm, int* counters, int n_cu, hipStream_t s);
+                              float* scratch, float* pm, hipStream_t s);
 hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, int n_kv, float* scratch, const float* pm,
                                int* counters, int n_cu, hipStream_t s);
 // ctx, or with `codes` set, ctx quantized per 32-dimension block straight into the o

@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
                                                        const float* __restrict__ w, float eps, int n,
                                                        ActQ8 a, float* __restrict__ y_opt)
 {
-    extern __shared__ float sx[];
+    extern __shared__ float sx[];  // the row, then its squares
     __shared__ float part[16];
     __shared__ float s_scale;
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -237,21 +237,38 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
         return;
     }
     const float* xr = x + (int64_t)t * ldx;
+    float* sq = sx + n;
     if (((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (n & 3) == 0) {
-        // float4 row copy, the loads of a thread issued together
+        // float4 row copy, the loads of a thread issued together; the squares x·x (rounded,
+        // as the reference's running sums add them) alongside
 #pragma unroll 4
-        for (int i = tid; i < n / 4; i += blockDim.x)
-            reinterpret_cast<float4*>(sx)[i] = reinterpret_cast<const float4*>(xr)[i];
+        for (int i = tid; i < n / 4; i += blockDim.x) {
+            const float4 v = reinterpret_cast<const float4*>(xr)[i];
+            reinterpret_cast<float4*>(sx)[i] = v;
+            reinterpret_cast<float4*>(sq)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+        }
     } else {
-        for (int i = tid; i < n; i += blockDim.x) sx[i] = xr[i];
+        for (int i = tid; i < n; i += blockDim.x) {
+            const float v = xr[i];
+            sx[i] = v;
+            sq[i] = v * v;
+        }
     }
     __syncthreads();
     if (tid < 16) {
+        // lane tid's running sum over elements tid + 16k in order; the reads of 16 steps are
+        // issued together, the adds stay one chain
         float acc = 0.0f;
-        for (int i = 0; i + 16 <= n; i += 16) {
-            float v = sx[i + tid];
-            acc = acc + v * v;
+        const int nk = n / 16;
+        int k = 0;
+        for (; k + 16 <= nk; k += 16) {
+            float v[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) v[q] = sq[(k + q) * 16 + tid];
+#pragma unroll
+            for (int q = 0; q < 16; q++) acc = acc + v[q];
         }
+        for (; k < nk; k++) acc = acc + sq[k * 16 + tid];
         part[tid] = acc;
     }
     __syncthreads();
@@ -285,7 +302,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float eps, int n, const ActQ8& a,
                                 float* y_opt, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(a.Tpad), dim3(256), sizeof(float) * n, s, x, ldx, w, eps, n, a, y_opt);
+    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(a.Tpad), dim3(256), 2 * sizeof(float) * n, s, x, ldx, w, eps, n, a, y_opt);
     return hipGetLastError();
 }
 
@@ -1838,10 +1855,10 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
         *reinterpret_cast<float4*>(outp + 8 * gq + 4 * h) = make_float4(o[4 * gq], o[4 * gq + 1], o[4 * gq + 2], o[4 * gq + 3]);
 }
 
-// The work of each attention kernel is handed out longest first from a counter, one item
-// per block at a time (greedy longest-processing-time order), so that the causal triangle's
-// long rows spread over all CUs whatever the hardware's block placement. Every block leaves
-// its loop once the counter passes the work count.
+// The softmax and value kernels of the three-kernel path take their work longest first
+// from a counter, one item per block at a time (greedy longest-processing-time order), so
+// that the causal triangle's long rows spread over all CUs whatever the hardware's block
+// placement. Every block leaves its loop once the counter passes the work count.
 __device__ __forceinline__ int next_work(int* counter, int* slot)
 {
     __syncthreads();  // the block is done with the previous item (and its LDS)
@@ -1854,7 +1871,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_scores(const float* __restrict_
                                                         int cap, const AttnItem* __restrict__ items,
                                                         const AttnChunk* __restrict__ chunks, int n_chunks, int n_head,
                                                         int n_kv, float scale, float* __restrict__ scratch,
-                                                        float* __restrict__ pm, int* __restrict__ counter)
+                                                        float* __restrict__ pm)
 {
     // one block per (chunk, KV head); the chunks come longest first, and the hardware hands
     // out blocks in order, so the causal triangle's long rows start first
@@ -1898,14 +1915,12 @@ static dim3 attn_blocks(int n_work, int per_cu, int n_cu)
 
 hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap, const AttnItem* items,
                               const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim, float scale,
-                              float* scratch, float* pm, int* counters, int n_cu, hipStream_t s)
+                              float* scratch, float* pm, hipStream_t s)
 {
     if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4) return hipErrorInvalidValue;
     if (n_chunks <= 0) return hipSuccess;
-    hipError_t e = launch_fill_zero(reinterpret_cast<float*>(counters), 3, s);  // the three work counters
-    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_scores, dim3((unsigned)(n_chunks * n_kv)), dim3(256), 0, s, q, ldq, kc, cap, items,
-                       chunks, n_chunks, n_head, n_kv, scale, scratch, pm, counters);
+                       chunks, n_chunks, n_head, n_kv, scale, scratch, pm);
     return hipGetLastError();
 }
 
@@ -1913,8 +1928,10 @@ hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, i
                                int* counters, int n_cu, hipStream_t s)
 {
     if (n_items <= 0) return hipSuccess;
+    hipError_t e = launch_fill_zero(reinterpret_cast<float*>(counters), 2, s);  // its and launch_attn_pv's counter
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_softmax, attn_blocks(n_items * n_head, 8, n_cu), dim3(256), 0, s, items, n_items, n_head,
-                       n_kv, scratch, pm, counters + 1);
+                       n_kv, scratch, pm, counters);
     return hipGetLastError();
 }
 
@@ -1926,7 +1943,7 @@ hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n
     if (codes && (codes->B != n_head * ATT_HD / 32 || !codes->q)) return hipErrorInvalidValue;
     const ActQ8 ao = codes ? *codes : ActQ8();
     hipLaunchKernelGGL(k_attn_pv, attn_blocks(n_items * (4 / ATT_PV_NSL) * n_kv, 5, n_cu), dim3(256), 0, s, vc, cap,
-                       items, n_items, n_head, n_kv, scratch, ctx, ldc, ao, counters + 2);
+                       items, n_items, n_head, n_kv, scratch, ctx, ldc, ao, counters + 1);
     return hipGetLastError();
 }
 
