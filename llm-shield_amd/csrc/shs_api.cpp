@@ -1135,9 +1135,26 @@ std::vector<AttnItem> causal_items(int q_begin, int n, int key_start, int pos0)
 // tile of 1024 floats per key tile), splits the items' key tiles into the score kernel's
 // chunks (longest items first, so they start first) and sizes the scratch: score tiles,
 // then 32 row maxima per tile.
+// The chunk length c (2..8 key tiles) minimizes rounds × (c + 1): the score kernel's blocks
+// fill its resident slots round by round, and a block costs about one tile more than its
+// tiles for its own start (the q and first K loads). Ties go to the shorter chunk.
 shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
 {
-    constexpr int kChunk = 4;
+    int kChunk = 4;
+    {
+        const int64_t slots = std::max(1, attn_score_slots(m->n_cu));
+        int64_t best = -1;
+        for (int c = 2; c <= 8; c++) {
+            int64_t blocks = 0;
+            for (const auto& it : items) blocks += ((it.pos0 + it.q_count + 31) / 32 + c - 1) / c;
+            blocks *= m->cfg.n_kv_head;
+            const int64_t cost = (blocks + slots - 1) / slots * (c + 1);
+            if (best < 0 || cost < best) {
+                best = cost;
+                kChunk = c;
+            }
+        }
+    }
     int64_t off = 0;
     for (auto& it : items) {
         it.s_off = off;

@@ -112,6 +112,8 @@ hipError_t launch_rope_store(float* qkv, int ldqkv, int T, int n_head, int n_kv_
 hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap, const AttnItem* items,
                               const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim, float scale,
                               float* scratch, float* pm, hipStream_t s);
+// Blocks of the score kernel resident on the whole device (per CU × n_cu).
+int attn_score_slots(int n_cu);
 hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, int n_kv, float* scratch, const float* pm,
                                int* counters, int n_cu, hipStream_t s);
 // ctx, or with `codes` set, ctx quantized per 32-dimension block straight into the o

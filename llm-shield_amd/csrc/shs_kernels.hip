@@ -1913,6 +1913,14 @@ static dim3 attn_blocks(int n_work, int per_cu, int n_cu)
     return dim3((unsigned)(n_work < per_cu * n_cu ? n_work : per_cu * n_cu));
 }
 
+int attn_score_slots(int n_cu)
+{
+    static int per_cu = 0;  // the same on every gfx950 device
+    if (per_cu == 0 && hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_attn_scores, 256, 0) != hipSuccess)
+        per_cu = 2;
+    return per_cu * n_cu;
+}
+
 hipError_t launch_attn_scores(const float* q, int ldq, const float* kc, int cap, const AttnItem* items,
                               const AttnChunk* chunks, int n_chunks, int n_head, int n_kv, int head_dim, float scale,
                               float* scratch, float* pm, hipStream_t s)
