@@ -78,6 +78,28 @@ def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
         assert (n_fused, n_split) == ((cfg.n_layer, 0) if fused else (0, cfg.n_layer)), (prefix, n)
 
 
+def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
+    """GQA groups below 4: the score kernel leaves a block's extra waves idle and the fused
+    softmax + values kernel skips the missing heads' blocks; both attention paths stay
+    bit-exact (a 40-token pass and a 1100-token one)."""
+    cfg = oracle.make_config(n_layer=1, hidden=256, n_head=4, n_kv_head=2, head_dim=128, ffn=512, vocab=512)
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=13)
+    gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=1200)
+    rng = np.random.default_rng(17)
+    ids = [0, 77, 300]
+    try:
+        for n in (40, 1100):
+            toks = rng.integers(0, cfg.vocab, n)
+            gpu.reset_kv_cache()
+            ora.reset()
+            g = gpu.forward_selected(toks, ids)
+            o = ora.forward(toks, head_mode=1, vocab_ids=ids)
+            assert np.array_equal(g, o), (n, H.rel_l2(g, o))
+    finally:
+        gpu.close()
+
+
 def test_selected_rows_are_bit_identical_to_the_full_head(shs, tiny):
     """SystemPromptCacheTests.ScoringReadsExactlyWhatTheFullHeadWouldHave."""
     cfg, tensors, types, gpu, ora = tiny
