@@ -6,6 +6,7 @@
 // 376-418), RMSNorm's accumulation order (Kernels.cs:26-61) and RoPE's rotation
 // (Rope.cs:112-135). The file is compiled with -ffp-contract=off; every fma is explicit.
 #include "shs_kernels.h"
+#include <type_traits>
 
 #include <math.h>
 
@@ -528,7 +529,7 @@ __device__ __forceinline__ void quant_block_pair(const float* y, int h, const Ac
 }
 
 template <int TYPE, int TT, int MODE>
-__global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+__global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                  const float* __restrict__ wd, const float* __restrict__ wm,
                                                  int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N,
                                                  int n_tg, ActQ8 ao, int n_ft, RopeArgs ra)
@@ -673,15 +674,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
     };
 
     for (int p = 0; p < NS - 1 && p < nstages; p++) issue(p, p);
-    for (int sidx = 0; sidx < nstages; ++sidx) {
+    // Stage sidx lives in ring slot sidx % NS; the loop below runs whole rounds of the ring
+    // with the slot a compile-time constant, so every LDS address is a fixed offset.
+    auto stage = [&](int sidx, auto slot_c) {
+        constexpr int SLOT = decltype(slot_c)::value;
         // stages issued after this one: NS − 2 in the steady state, fewer at the end
         const int ahead = nstages - 1 - sidx;
         if (ahead >= 2) wait_copies_barrier<2 * L::PER_STAGE>();
         else if (ahead == 1) wait_copies_barrier<L::PER_STAGE>();
         else wait_copies_barrier<0>();
-        if (sidx + NS - 1 < nstages) issue(sidx + NS - 1, (sidx + NS - 1) % NS);
-        if (!active) continue;
-        const uint8_t* base = ring + (sidx % NS) * L::BYTES;
+        if (sidx + NS - 1 < nstages) issue(sidx + NS - 1, (SLOT + NS - 1) % NS);
+        if (!active) return;
+        const uint8_t* base = ring + SLOT * L::BYTES;
         const float* da_s = reinterpret_cast<const float*>(base + L::ACT + L::CV);
         const float* dw_s = reinterpret_cast<const float*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX);
         // A block past B (odd B, last stage) holds copies of block B−1: its d_w is taken as 0,
@@ -723,7 +727,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm(const uint8_t* __restrict__ wqs
             for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G1[r], S[16 + r], acc[0][r]);
             if (OFF) offset_term(base, 1, 0, valid1);
         }
+    };
+    static_assert(NS == 4, "the rounds below are written out for four slots");
+    typedef std::integral_constant<int, 0> S0;
+    typedef std::integral_constant<int, 1> S1;
+    typedef std::integral_constant<int, 2> S2;
+    typedef std::integral_constant<int, 3> S3;
+    int sidx = 0;
+    for (; sidx + NS <= nstages; sidx += NS) {
+        stage(sidx, S0());
+        stage(sidx + 1, S1());
+        stage(sidx + 2, S2());
+        stage(sidx + 3, S3());
     }
+    if (sidx < nstages) stage(sidx, S0());
+    if (sidx + 1 < nstages) stage(sidx + 1, S1());
+    if (sidx + 2 < nstages) stage(sidx + 2, S2());
     const int nv = ntt - tt0 < TT ? ntt - tt0 : TT;
     if constexpr (MODE == GEMM_SWIGLU) {
         // Exchange the accumulators through the (now idle) ring: X[wave][u][r][lane]; then
