@@ -971,8 +971,12 @@ hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy
     }
 }
 
+static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s);
+
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
 {
+    if ((mode == GEMM_STORE || mode == GEMM_ADD) && gemm_narrow_tokens(w, a) > 0)
+        return launch_gemm_narrow(w, a, y, ldy, mode, s);
     switch (w.type) {
     case SHS_TYPE_Q4_0: return gemm_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s);
     case SHS_TYPE_Q4_1: return gemm_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s);
@@ -1112,6 +1116,244 @@ hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* i
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+// ------------------------------------------------- narrow GEMM (decode, T ≤ 4)
+
+// Bytes of dynamic LDS k_gemm_narrow<.., R> needs for B blocks and nt tokens: the activation
+// codes, then per (token, row, block) the pair (I, RN(d_w·d_a)), then m_w per (row, block)
+// for the offset types, then Σa, d_a and RN(d_a·Σa) per (token, block).
+static size_t narrow_lds_bytes(int R, int B, int nt, bool off)
+{
+    const size_t pb = (size_t)B + 1;
+    return 32 * (size_t)nt * B + 8 * (size_t)nt * R * pb + (off ? 4 * (size_t)R * pb : 0) + 4 * (size_t)nt * B * 3;
+}
+
+// Rows per work-group: 8 for the layer projections (many work-groups for a few MB of
+// weights), 32 for matrices of 64k rows and more (the vocabulary head: one tile per
+// work-group, its activation staging spread over 4× the weights).
+static int narrow_rows(const DevMatrix& w) { return w.rows >= 65536 ? 32 : 8; }
+
+// One batch of a thread's row-blocks: blocks b0 + j·(256/R), j < 4, clamped to the last
+// block (a clamped load re-reads a line the work-group already has).
+template <int TYPE>
+struct NarrowBatch {
+    uint4 q[4], q8[4];
+    uint32_t qh[4];
+    float dw[4], mw[4];
+};
+
+template <int TYPE, int R>
+__device__ __forceinline__ void narrow_load(NarrowBatch<TYPE>& nb, const uint8_t* __restrict__ wqs,
+                                            const uint32_t* __restrict__ wqh, const float* __restrict__ wd,
+                                            const float* __restrict__ wm, int64_t rec0, int ri, int b0, int B)
+{
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t rec = rec0 + min(b0 + j * (256 / R), B - 1);
+        if (TYPE == SHS_TYPE_Q8_0) {
+            nb.q[j] = *reinterpret_cast<const uint4*>(wqs + rec * 1024 + ri * 32);
+            nb.q8[j] = *reinterpret_cast<const uint4*>(wqs + rec * 1024 + ri * 32 + 16);
+        } else {
+            nb.q[j] = *reinterpret_cast<const uint4*>(wqs + rec * 512 + ri * 16);
+        }
+        if (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1) nb.qh[j] = wqh[rec * 32 + ri];
+        nb.dw[j] = wd[rec * 32 + ri];
+        if (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1) nb.mw[j] = wm[rec * 32 + ri];
+    }
+}
+
+// y = x·Wᵀ (mode 0 store, 1 add into y) for NT ≤ 4 tokens: single-token decode and the
+// full-vocabulary head at the last position. At this width the weights are streamed once
+// from HBM and the int8 MFMA's 32-token tiles would be mostly padding, so a work-group takes
+// R rows × all blocks:
+// - the first batch of weight loads is issued, then the activation codes, d_a, Σa (from the
+//   conversion column) and RN(d_a·Σa) are staged in the LDS under its latency;
+// - phase 1: thread (row r = tid % R, blocks b ≡ tid / R mod 256/R, four per batch, the next
+//   batch loading while this one computes) forms the exact block sums I = Σu·a − z·Σa of
+//   every token with v_dot4 and the scale RN(d_w·d_a) into the LDS;
+// - phase 2: lane (t, r) runs the reference's chain acc = fma(I_b, RN(d_w·d_a), acc)
+//   [then fma(m_w, RN(d_a·Σa), acc) for the offset types] over b in order
+//   (IntegerGemm.cs:384-397) — k_gemm's arithmetic, so an output does not depend on the
+//   path that computed it.
+// The grid is a multiple of 8 and work-group g of the logical order runs on XCD g / (grid/8):
+// the work-groups of a 32-row tile share its d (and qh, m) lines in one L2.
+template <int TYPE, int NT, int MODE, int R>
+__global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+                                                     const float* __restrict__ wd, const float* __restrict__ wm,
+                                                     int rows, int B, int n_wg, ActQ8 a, float* __restrict__ y, int ldy)
+{
+    constexpr bool OFF = TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1;
+    constexpr bool Q8 = TYPE == SHS_TYPE_Q8_0;
+    constexpr int Z = ZeroPoint<TYPE>::z;
+    constexpr int BS = 256 / R;  // block stride between a thread's row-blocks
+    const int g = (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
+    if (g >= n_wg) return;
+    extern __shared__ uint4 nw_lds[];
+    const int PB = B + 1;  // odd float2 stride: the chain lanes read different banks
+    uint4* sA = nw_lds;                                              // [NT][B][2 halves] codes
+    float2* sP = reinterpret_cast<float2*>(sA + NT * B * 2);         // [NT][R][PB] (I, RN(d_w·d_a))
+    float* sM = reinterpret_cast<float*>(sP + NT * R * PB);          // [R][PB] m_w
+    int* sSum = reinterpret_cast<int*>(sM + (OFF ? R * PB : 0));     // [NT][B] Σa
+    float* sDa = reinterpret_cast<float*>(sSum + NT * B);            // [NT][B] d_a
+    float* sDs = sDa + NT * B;                                       // [NT][B] RN(d_a·Σa)
+    const int tid = threadIdx.x;
+    const int r = tid % R, bl = tid / R;
+    const int row = g * R + r;  // < tiles·32: n_wg covers the padded rows exactly
+    const int64_t rec0 = (int64_t)(row >> 5) * B;
+    const int ri = row & 31;
+
+    NarrowBatch<TYPE> cur, nxt;
+    narrow_load<TYPE, R>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
+
+    for (int i = tid; i < NT * B * 2; i += 256) {
+        const int t = i / (2 * B), rem = i - t * 2 * B, b = rem >> 1, h = rem & 1;
+        sA[i] = *reinterpret_cast<const uint4*>(a.q + (((int64_t)(t >> 5) * B + b) * 64 + (t & 31)) * 16 + h * 512);
+    }
+    for (int i = tid; i < NT * B; i += 256) {
+        const int t = i / B, b = i - t * B;
+        const int64_t k = (int64_t)b * a.Tpad + t;
+        sDa[i] = a.d[k];
+        if (OFF) sDs[i] = a.ds[k];
+        if (Z != 0) {
+            // the conversion column holds fp16 (−6144, −hi, −lo, 0) with Σa = 64·hi + lo
+            const uint2 cv = a.cv[k];
+            const int hi = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(cv.x >> 16));
+            const int lo = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(cv.y & 0xFFFFu));
+            sSum[i] = -(64 * hi + lo);
+        }
+    }
+    __syncthreads();
+
+    for (int b0 = bl; b0 < B; b0 += 4 * BS) {
+        narrow_load<TYPE, R>(nxt, wqs, wqh, wd, wm, rec0, ri, min(b0 + 4 * BS, B - 1), B);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = b0 + j * BS;
+            if (b < B) {
+                const v4i w0 = Q8 ? v4i{(int)cur.q[j].x, (int)cur.q[j].y, (int)cur.q[j].z, (int)cur.q[j].w}
+                                  : weights_i8<TYPE>(cur.q[j].x, cur.q[j].y, 0u, 0u, cur.qh[j], 0);
+                const v4i w1 = Q8 ? v4i{(int)cur.q8[j].x, (int)cur.q8[j].y, (int)cur.q8[j].z, (int)cur.q8[j].w}
+                                  : weights_i8<TYPE>(cur.q[j].z, cur.q[j].w, 0u, 0u, cur.qh[j], 1);
+                if (OFF) sM[r * PB + b] = cur.mw[j];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const uint4 a0 = sA[(t * B + b) * 2], a1 = sA[(t * B + b) * 2 + 1];
+                    int s = 0;
+                    s = __builtin_amdgcn_sdot4(w0[0], (int)a0.x, s, false);
+                    s = __builtin_amdgcn_sdot4(w0[1], (int)a0.y, s, false);
+                    s = __builtin_amdgcn_sdot4(w0[2], (int)a0.z, s, false);
+                    s = __builtin_amdgcn_sdot4(w0[3], (int)a0.w, s, false);
+                    s = __builtin_amdgcn_sdot4(w1[0], (int)a1.x, s, false);
+                    s = __builtin_amdgcn_sdot4(w1[1], (int)a1.y, s, false);
+                    s = __builtin_amdgcn_sdot4(w1[2], (int)a1.z, s, false);
+                    s = __builtin_amdgcn_sdot4(w1[3], (int)a1.w, s, false);
+                    if (Z != 0) s -= Z * sSum[t * B + b];
+                    sP[(t * R + r) * PB + b] = make_float2((float)s, cur.dw[j] * sDa[t * B + b]);
+                }
+            }
+        }
+        cur = nxt;
+    }
+    __syncthreads();
+
+    if (tid < NT * R) {
+        const int t = tid / R, rr = tid % R;
+        const float2* p = sP + (t * R + rr) * PB;
+        const float* pm = sM + rr * PB;
+        const float* pd = sDs + t * B;
+        float acc = 0.0f;
+        // the chain's operands are read 16 steps at a time, so LDS latency is paid once per 16
+        int b = 0;
+        for (; b + 16 <= B; b += 16) {
+            float2 v[16];
+            float m[16], ds[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                v[k] = p[b + k];
+                if (OFF) {
+                    m[k] = pm[b + k];
+                    ds[k] = pd[b + k];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                acc = fmaf(v[k].x, v[k].y, acc);
+                if (OFF) acc = fmaf(m[k], ds[k], acc);
+            }
+        }
+        for (; b < B; ++b) {
+            const float2 v = p[b];
+            acc = fmaf(v.x, v.y, acc);
+            if (OFF) acc = fmaf(pm[b], pd[b], acc);
+        }
+        const int orow = g * R + rr;
+        if (orow < rows) {
+            float* dst = y + (int64_t)t * ldy + orow;
+            *dst = MODE == GEMM_ADD ? *dst + acc : acc;
+        }
+    }
+}
+
+template <int TYPE, int NT, int MODE, int R>
+static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+{
+    constexpr bool OFF = TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1;
+    const int n_wg = w.tiles * (32 / R);
+    const size_t shm = narrow_lds_bytes(R, w.blocks, NT, OFF);
+    if (shm > (64u << 10)) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_narrow<TYPE, NT, MODE, R>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+        if (e != hipSuccess) return e;
+    }
+    dim3 grid((unsigned)((n_wg + 7) / 8 * 8)), block(256);
+    hipLaunchKernelGGL((k_gemm_narrow<TYPE, NT, MODE, R>), grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.rows,
+                       w.blocks, n_wg, a, y, ldy);
+    return hipGetLastError();
+}
+
+template <int TYPE, int NT, int MODE>
+static hipError_t narrow_rows_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+{
+    return narrow_rows(w) == 32 ? narrow_launch<TYPE, NT, MODE, 32>(w, a, y, ldy, s)
+                                : narrow_launch<TYPE, NT, MODE, 8>(w, a, y, ldy, s);
+}
+
+template <int TYPE, int MODE>
+static hipError_t narrow_mode(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+{
+    switch (a.T) {
+    case 1: return narrow_rows_launch<TYPE, 1, MODE>(w, a, y, ldy, s);
+    case 2: return narrow_rows_launch<TYPE, 2, MODE>(w, a, y, ldy, s);
+    case 3: return narrow_rows_launch<TYPE, 3, MODE>(w, a, y, ldy, s);
+    case 4: return narrow_rows_launch<TYPE, 4, MODE>(w, a, y, ldy, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int TYPE>
+static hipError_t narrow_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+{
+    return mode == GEMM_ADD ? narrow_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s) : narrow_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s);
+}
+
+static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+{
+    switch (w.type) {
+    case SHS_TYPE_Q4_0: return narrow_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q4_1: return narrow_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q5_0: return narrow_type<SHS_TYPE_Q5_0>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q5_1: return narrow_type<SHS_TYPE_Q5_1>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q8_0: return narrow_type<SHS_TYPE_Q8_0>(w, a, y, ldy, mode, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a)
+{
+    if (a.T < 1 || a.T > NARROW_MAX_T || !type_supported(w.type)) return 0;
+    const bool off = type_has_offset(w.type);
+    return narrow_lds_bytes(narrow_rows(w), w.blocks, a.T, off) <= (160u << 10) ? a.T : 0;
 }
 
 // -------------------------------------------------------- embedding gather

@@ -84,6 +84,25 @@ def test_a_tokens_result_does_not_depend_on_the_batch(lib, oracle, qt):
 
 
 @pytest.mark.parametrize("qt", TYPES)
+def test_decode_widths_are_bit_exact(lib, oracle, qt):
+    """1-4 tokens take the weight-streaming narrow kernel: bit-exact against the oracle and
+    against the same tokens inside a wide batch, with a partial row tile, an odd block
+    count (7), the down projection's 288 blocks and a head-sized row count (32-row
+    work-groups from 65536 rows)."""
+    rng = np.random.default_rng(20 + qt)
+    for rows, cols in [(100, 3072), (64, 224), (40, 9216), (65601, 256)]:
+        w = H.random_blocks(qt, rows, cols, seed=rows + cols + qt)
+        m = lib.WeightMatrix(qt, rows, cols, w)
+        x = (rng.random((40, cols)) * 2 - 1).astype(np.float32)
+        wide = m.forward(x)
+        for T in (1, 2, 3, 4):
+            y = m.forward(x[:T])
+            ref = oracle.matmul(qt, w, rows, cols, x[:T], T)
+            assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), (rows, cols, T)
+            assert np.array_equal(y, wide[:T]), (rows, cols, T)
+
+
+@pytest.mark.parametrize("qt", TYPES)
 def test_a_row_subset_is_bit_identical_to_the_full_product(lib, oracle, qt):
     """MatMulTilingTests.ARowSubsetIsBitIdenticalToTheFullProduct."""
     rows, cols, T = 100, 256, 5

@@ -112,6 +112,26 @@ def test_selected_rows_are_bit_identical_to_the_full_head(shs, tiny):
     assert np.array_equal(sel, full[ids])
 
 
+def test_single_token_decode_matches_the_oracle(shs, tiny):
+    """Benchmark.cs:399-410's decode: single-token forwards (full-vocabulary logits) onto a
+    prefilled cache, then a 3-token step — the narrow GEMM path with unfused RoPE and SwiGLU
+    — bit-exact against the oracle stepping its own cache the same way."""
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(12).integers(0, cfg.vocab, 60)
+    gpu.reset_kv_cache()
+    ora.reset()
+    assert np.array_equal(gpu.forward(toks[:50]), ora.forward(toks[:50], head_mode=2))
+    for i in range(50, 57):
+        g = gpu.forward(toks[i:i + 1])
+        o = ora.forward(toks[i:i + 1], head_mode=2)
+        assert np.array_equal(g.view(np.uint32), o.view(np.uint32)), i
+    last = gpu.forward(toks[57:60])
+    assert np.array_equal(last, ora.forward(toks[57:60], head_mode=2))
+    assert gpu.cached_token_count == 60
+    gpu.reset_kv_cache()
+    assert np.array_equal(gpu.forward(toks), last)  # the same position through the wide kernels
+
+
 def test_prefix_cache_is_bit_identical(shs, tiny):
     """SystemPromptCacheTests.CachedAndUncachedProduceIdenticalLogits (all vocab entries)."""
     cfg, tensors, types, gpu, ora = tiny
