@@ -349,6 +349,9 @@ struct shs_model {
     int n_cu = 0;          // compute units of the device (persistent kernel sizing)
     int fused_kt = 0;      // most key tiles an item may have for the fused softmax + values kernel
     int max_kt = 0;        // key tiles of the longest placed item
+    int max_lds = 0;       // LDS bytes a block may use (opt-in)
+    int max_qc = 0;        // queries of the widest placed item
+    int max_keys = 0;      // keys of the longest placed item
     int64_t score_floats = 0, pm_floats = 0;
     int64_t attn_pairs = 0;
     ActBuf act;
@@ -643,7 +646,8 @@ shs_status build_model(const shs_config& c, const SpecMap& tm, int device, int i
         if ((e = hipDeviceGetAttribute(&optin, hipDeviceAttributeSharedMemPerBlockOptin, device)) != hipSuccess) optin = 0;
         if ((e = hipDeviceGetAttribute(&base, hipDeviceAttributeMaxSharedMemoryPerBlock, device)) != hipSuccess)
             return bail(hip_fail(e, "hipDeviceGetAttribute"));
-        m->fused_kt = attn_fused_kt_limit(std::max(optin, base));
+        m->max_lds = std::max(optin, base);
+        m->fused_kt = attn_fused_kt_limit(m->max_lds);
     }
     if ((e = m->counters.ensure(64)) != hipSuccess) return bail(hip_fail(e, "hipMalloc(counters)"));
     m->layers.reserve(c.n_layer);
@@ -1010,27 +1014,36 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             int* ctr = m->counters.as<int>();
             // 2·head_dim flops per (query, key) pair and head, for the scores and again for the values
             const double attn_ops = 2.0 * c.head_dim * c.n_head * (double)m->attn_pairs;
-            {
-                Timed tk(m->prof, "k_attn_scores", attn_ops, m->stream, "attention");
-                HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(), m->n_chunks,
-                                           c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, m->stream));
-            }
-            // without capture, the value step writes the o projection's activation codes itself
-            if (m->max_kt <= m->fused_kt) {
-                // every item's scores fit one block's LDS: softmax and values in one kernel
-                Timed tk(m->prof, "k_attn_softmax_pv", attn_ops, m->stream, "attention");
-                HIP_TRY(launch_attn_softmax_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctx, qdim,
-                                               cap_on ? nullptr : &ac, m->max_kt, m->stream));
+            if (m->max_qc <= ATT_DEC_MAX_Q && c.n_head / c.n_kv_head <= 4 &&
+                m->max_keys <= attn_decode_max_keys(m->max_qc, m->max_lds)) {
+                // decode width: scores per (KV head, 64-key chunk), values per (head, 32-dim slice)
+                Timed tk(m->prof, "k_attn_decode", attn_ops, m->stream, "attention");
+                HIP_TRY(launch_attn_decode(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head,
+                                           c.head_dim, scale, m->max_qc, m->max_keys, scr, ctx, qdim,
+                                           cap_on ? nullptr : &ac, m->stream));
             } else {
                 {
-                    Timed tk(m->prof, "k_attn_softmax", 0, m->stream, "attention");
-                    HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu,
-                                                m->stream));
+                    Timed tk(m->prof, "k_attn_scores", attn_ops, m->stream, "attention");
+                    HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(), m->n_chunks,
+                                               c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, m->stream));
                 }
-                {
-                    Timed tk(m->prof, "k_attn_pv", attn_ops, m->stream, "attention");
-                    HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim,
-                                           cap_on ? nullptr : &ac, ctr, m->n_cu, m->stream));
+                // without capture, the value step writes the o projection's activation codes itself
+                if (m->max_kt <= m->fused_kt) {
+                    // every item's scores fit one block's LDS: softmax and values in one kernel
+                    Timed tk(m->prof, "k_attn_softmax_pv", attn_ops, m->stream, "attention");
+                    HIP_TRY(launch_attn_softmax_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctx, qdim,
+                                                   cap_on ? nullptr : &ac, m->max_kt, m->stream));
+                } else {
+                    {
+                        Timed tk(m->prof, "k_attn_softmax", 0, m->stream, "attention");
+                        HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu,
+                                                    m->stream));
+                    }
+                    {
+                        Timed tk(m->prof, "k_attn_pv", attn_ops, m->stream, "attention");
+                        HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim,
+                                               cap_on ? nullptr : &ac, ctr, m->n_cu, m->stream));
+                    }
                 }
             }
         }
@@ -1174,8 +1187,12 @@ shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
     }
     m->score_floats = off;
     m->pm_floats = off / 32;
-    m->max_kt = 0;
-    for (const auto& it : items) m->max_kt = std::max(m->max_kt, (it.pos0 + it.q_count + 31) / 32);
+    m->max_kt = m->max_qc = m->max_keys = 0;
+    for (const auto& it : items) {
+        m->max_kt = std::max(m->max_kt, (it.pos0 + it.q_count + 31) / 32);
+        m->max_qc = std::max(m->max_qc, it.q_count);
+        m->max_keys = std::max(m->max_keys, it.pos0 + it.q_count);
+    }
     m->attn_pairs = 0;  // (query, key) pairs the items attend over
     for (const auto& it : items) m->attn_pairs += (int64_t)it.q_count * it.pos0 + (int64_t)it.q_count * (it.q_count + 1) / 2;
     HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off + m->pm_floats, 1)));

@@ -133,6 +133,17 @@ hipError_t launch_attn_softmax_pv(const float* vc, int cap, const AttnItem* item
                                   const float* scratch, const float* pm, float* ctx, int ldc, const ActQ8* codes,
                                   int kt_cap, hipStream_t s);
 int attn_fused_kt_limit(int max_lds_bytes);
+// Attention for items of at most ATT_DEC_MAX_Q queries (decode), at most 4 query heads per
+// KV head: a score kernel over (item, KV head, 64-key chunk) writing the scores to the
+// scratch (each item's region from place_items), then softmax + values over (item, query
+// head, 32-dimension slice). Every item must have at most max_qc queries and max_keys keys,
+// max_keys at most attn_decode_max_keys(max_qc, the device's LDS per block). ctx, or with
+// `codes` set, the o projection's codes of the items' rows.
+enum { ATT_DEC_MAX_Q = 4 };
+int attn_decode_max_keys(int max_qc, int max_lds_bytes);
+hipError_t launch_attn_decode(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
+                              int n_items, int n_head, int n_kv, int head_dim, float scale, int max_qc, int max_keys,
+                              float* scratch, float* ctx, int ldc, const ActQ8* codes, hipStream_t s);
 hipError_t launch_expf(const float* x, int n, float* y, hipStream_t s);
 hipError_t launch_copy_rows(const float* src, int lds, float* dst, int ldd, int rows, int cols, hipStream_t s);
 hipError_t launch_fill_zero(float* p, size_t n, hipStream_t s);

@@ -134,6 +134,60 @@ __device__ __forceinline__ int64_t act_code_offset(const ActQ8& a, int t, int b,
     return ((((int64_t)(t >> 5) * a.B + b) * 2 + h) * 32 + (t & 31)) * 16 + idx;
 }
 
+// Lane exchanges on the DPP path (an operand modifier of a VALU instruction, no LDS round
+// trip as __shfl takes), for reductions over aligned lane groups: quad_perm [1,0,3,2] swaps
+// neighbours (xor 1), [2,3,0,1] swaps pairs (xor 2), row_half_mirror maps lane i of an
+// 8-lane group to 7 − i and row_mirror lane i of a 16-lane row to 15 − i. After the two quad
+// steps of a reduction every lane of a quad holds the same value, so the mirrors then pair
+// quads like xor 4 and xor 8 would.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// max over the 64 lanes of a wave (NaN lanes are ignored, as fmaxf does), in every lane
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+__device__ __forceinline__ int wave_or(int v)
+{
+    v |= dpp_i<DPP_XOR1>(v);
+    v |= dpp_i<DPP_XOR2>(v);
+    v |= dpp_i<DPP_HALF_MIRROR>(v);
+    v |= dpp_i<DPP_MIRROR>(v);
+    return __builtin_amdgcn_readlane(v, 0) | __builtin_amdgcn_readlane(v, 16) | __builtin_amdgcn_readlane(v, 32) |
+           __builtin_amdgcn_readlane(v, 48);
+}
+
+// vsum8's ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)) of an aligned 8-lane group holding a_t in
+// lane t, in every lane of the group (each addition is commutative, so the lanes agree)
+__device__ __forceinline__ float vsum8_lanes(float v)
+{
+    v = v + dpp_f<DPP_XOR1>(v);
+    v = v + dpp_f<DPP_XOR2>(v);
+    return v + dpp_f<DPP_HALF_MIRROR>(v);
+}
+
 // One 32-value block: IntegerGemm.QuantizeActivations (semantics 0: d = max|x|/127,
 // q = RNE(x·(1/d)), IntegerGemm.cs:97-138) or IntegerDot.QuantizeActivations (1: q rounded
 // half away from zero and clamped to ±127, d rounded to fp16, IntegerDot.cs:60-98); d and
@@ -144,9 +198,9 @@ __device__ __forceinline__ int64_t act_code_offset(const ActQ8& a, int t, int b,
 __device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, int t, int b, int semantics)
 {
     float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 8));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 8));
-    mx = fmaxf(mx, __shfl_xor(mx, 4, 8));
+    mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+    mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+    mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
     const float d = mx / 127.0f;
     const float inv = d != 0.0f ? 1.0f / d : 0.0f;
     int q0, q1, q2, q3;
@@ -165,9 +219,9 @@ __device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, i
         dd = round_to_half(d);
     }
     int sum = (q0 + q1) + (q2 + q3);
-    sum += __shfl_xor(sum, 1, 8);
-    sum += __shfl_xor(sum, 2, 8);
-    sum += __shfl_xor(sum, 4, 8);
+    sum += dpp_i<DPP_XOR1>(sum);
+    sum += dpp_i<DPP_XOR2>(sum);
+    sum += dpp_i<DPP_HALF_MIRROR>(sum);
     const uint32_t w = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
                        ((uint32_t)(q3 & 0xFF) << 24);
     *reinterpret_cast<uint32_t*>(a.q + act_code_offset(a, t, b, l8)) = w;
@@ -1697,10 +1751,15 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
         mx = fmaxf(mx, v);
         nan = nan || v != v;
     }
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o, 8));
-        nan = nan || __shfl_xor((int)nan, o, 8);
+    mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+    mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+    mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+    {
+        int nn = nan ? 1 : 0;
+        nn |= dpp_i<DPP_XOR1>(nn);
+        nn |= dpp_i<DPP_XOR2>(nn);
+        nn |= dpp_i<DPP_HALF_MIRROR>(nn);
+        nan = nn != 0;
     }
     const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);  // Kernels.Softmax: a non-finite max
 
@@ -1743,9 +1802,7 @@ __device__ __forceinline__ void attn_softmax_work(int idx, int head, const AttnI
     }
     // vsum8: ((a0+a1)+(a2+a3))+((a4+a5)+(a6+a7)); addition is commutative, so each lane
     // forms its pair with its xor partner.
-    float total = lane_sum + __shfl_xor(lane_sum, 1, 8);
-    total = total + __shfl_xor(total, 2, 8);
-    total = total + __shfl_xor(total, 4, 8);
+    float total = vsum8_lanes(lane_sum);
     // the tail keys n8 .. nq−1 in order; lane k holds key n8 + k
 #pragma unroll
     for (int k = 0; k < 7; k++) {
@@ -1926,10 +1983,15 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
             mx = fmaxf(mx, v);
             nan = nan || v != v;
         }
-#pragma unroll
-        for (int o = 1; o < 8; o <<= 1) {
-            mx = fmaxf(mx, __shfl_xor(mx, o, 8));
-            nan = nan || __shfl_xor((int)nan, o, 8);
+        mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+        mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
+        mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
+        {
+            int nn = nan ? 1 : 0;
+            nn |= dpp_i<DPP_XOR1>(nn);
+            nn |= dpp_i<DPP_XOR2>(nn);
+            nn |= dpp_i<DPP_HALF_MIRROR>(nn);
+            nan = nn != 0;
         }
         const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);
         const int64_t rec = (int64_t)j * 32 + t * 4;
@@ -1980,9 +2042,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
                 *reinterpret_cast<float4*>(S + (kt0 + q) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
             }
         }
-        float total = lane_sum + __shfl_xor(lane_sum, 1, 8);
-        total = total + __shfl_xor(total, 2, 8);
-        total = total + __shfl_xor(total, 4, 8);
+        float total = vsum8_lanes(lane_sum);
 #pragma unroll
         for (int k = 0; k < 7; k++) {
             const float e = __shfl(tail_e, k, 8);
@@ -2242,6 +2302,320 @@ hipError_t launch_attn_softmax_pv(const float* vc, int cap, const AttnItem* item
     const unsigned grid = (unsigned)(((n_groups + 7) / 8) * 32);
     hipLaunchKernelGGL(k_attn_softmax_pv, dim3(grid), dim3(256), lds, s, vc, cap, items, n_items, n_head, n_kv, scratch,
                        pm, ctx, ldc, ao, kt_cap);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------ attention at decode width
+
+// Items of at most ATT_DEC_MAX_Q queries (single-token decode, a few tokens per sequence)
+// skip the 32-query tiles above, which would be almost all padding. At this width the cost
+// is memory latency, so the work is spread over many blocks with all their loads issued up
+// front, in two kernels:
+//  1. k_attn_dec_scores, one block per (item, KV head, 64-key chunk): the chunk's K rows
+//     (coalesced) and the group's q rows go to the LDS; lane i of a key's 4 lanes runs Dot4's
+//     chains 2i and 2i+1, c_l = fma(k[l+8m], q[l+8m], c_l) for m = 0..15, the 4 lanes add
+//     pairwise in vsum8's order and the scale follows (MinistralModel.cs:392-405,
+//     Kernels.cs:103-122); every query head of the group and every query of the item;
+//  2. k_attn_dec_pv, one block per (item, query head, 32-dimension slice): the slice of V is
+//     loaded while the block forms the softmax of the head's scores — max; e = exp(s − max)
+//     (1 when the max is not finite); Σe over 8 lanes of residues in key order, pairwise,
+//     then the tail in order; w = e / Σe correctly rounded (Kernels.cs:157-200) — then lane
+//     (query, dimension) runs ctx = fma(v, w, ctx) over the keys in order (Kernels.AddScaled4).
+//     A slice is one 32-dimension block of the o projection's input, quantized in place when
+//     codes are given.
+// Scores go to the item's scratch region as [head][query][ld_k], ld_k = keys rounded up to 4.
+constexpr int DEC_KT = 64;             // keys per score block
+constexpr int DEC_KROW = ATT_HD + 8;   // padded K row: 8 consecutive keys start 8 banks apart
+constexpr int DEC_VCH = 256;           // keys per staged V chunk
+
+__device__ __forceinline__ int dec_ld_k(const AttnItem& it) { return (it.pos0 + it.q_count + 3) & ~3; }
+
+__global__ __launch_bounds__(256) void k_attn_dec_scores(const float* __restrict__ q, int ldq,
+                                                         const float* __restrict__ kc, int cap,
+                                                         const AttnItem* __restrict__ items, int n_head, int n_kv,
+                                                         int n_chunks, float scale, float* __restrict__ scratch)
+{
+    const int G = n_head / n_kv;
+    const int b = blockIdx.x;
+    const int idx = b / (n_kv * n_chunks), r = b % (n_kv * n_chunks);
+    const int kvh = r / n_chunks, ch = r % n_chunks;
+    const AttnItem it = items[idx];
+    const int qc = it.q_count, nk = it.pos0 + qc;
+    if (ch * DEC_KT >= nk) return;
+    extern __shared__ float dsk[];
+    float* sK = dsk;                      // [DEC_KT][DEC_KROW]
+    float* sQ = dsk + DEC_KT * DEC_KROW;  // [G·qc][128]
+    const int tid = threadIdx.x;
+    const float* kb = kc + ((int64_t)kvh * cap + it.key_start) * ATT_HD;
+    // K rows ch·64 .. +63: float4 e = tid + 256j is key e / 32, columns 4(e % 32) .. +3
+    v4f kr[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int e = tid + 256 * j;
+        const int key = min(ch * DEC_KT + (e >> 5), nk - 1);
+        kr[j] = *reinterpret_cast<const v4f*>(kb + (int64_t)key * ATT_HD + 4 * (e & 31));
+    }
+    for (int i = tid; i < G * qc * (ATT_HD / 4); i += 256) {
+        const int hq = i / (ATT_HD / 4), u = i % (ATT_HD / 4);
+        const int hg = hq / qc, qi = hq % qc;
+        reinterpret_cast<v4f*>(sQ)[i] = *reinterpret_cast<const v4f*>(
+            q + (int64_t)(it.q_start + qi) * ldq + (kvh * G + hg) * ATT_HD + 4 * u);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int e = tid + 256 * j;
+        *reinterpret_cast<v4f*>(sK + (e >> 5) * DEC_KROW + 4 * (e & 31)) = kr[j];
+    }
+    __syncthreads();
+    const int kk = tid >> 2, ci = tid & 3;
+    const int key = ch * DEC_KT + kk;
+    const int ld_k = dec_ld_k(it);
+    const float2* krow = reinterpret_cast<const float2*>(sK + kk * DEC_KROW + 2 * ci);
+    for (int hq = 0; hq < G * qc; hq++) {
+        const int hg = hq / qc, qi = hq % qc;
+        const float2* qrow = reinterpret_cast<const float2*>(sQ + hq * ATT_HD + 2 * ci);
+        float c0 = 0.0f, c1 = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 16; m++) {
+            const float2 kv = krow[4 * m], qv = qrow[4 * m];
+            c0 = fmaf(kv.x, qv.x, c0);
+            c1 = fmaf(kv.y, qv.y, c1);
+        }
+        // vsum8: ((c0+c1)+(c2+c3))+((c4+c5)+(c6+c7)); lane i holds c_2i + c_2i+1
+        float p = c0 + c1;
+        p = p + dpp_f<DPP_XOR1>(p);
+        p = p + dpp_f<DPP_XOR2>(p);
+        if (ci == 0 && key <= it.pos0 + qi)
+            scratch[it.s_off + ((int64_t)(kvh * G + hg) * qc + qi) * ld_k + key] = p * scale;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_attn_dec_pv(const float* __restrict__ vc, int cap,
+                                                     const AttnItem* __restrict__ items, int n_head, int n_kv,
+                                                     int ld_s, int max_qc, const float* __restrict__ scratch,
+                                                     float* __restrict__ ctx, int ldc, ActQ8 ao)
+{
+    constexpr int NSL = ATT_HD / 32;
+    const int G = n_head / n_kv;
+    const int b = blockIdx.x;
+    const int idx = b / (n_head * NSL), r = b % (n_head * NSL);
+    const int head = r / NSL, sl = r % NSL;
+    const int kvh = head / G;
+    const AttnItem it = items[idx];
+    const int qc = it.q_count, nk = it.pos0 + qc;
+    const int ld_k = dec_ld_k(it);
+    extern __shared__ float dpv[];
+    float* sW = dpv;                          // [qc][ld_s] scores → e → w
+    float* sV = dpv + max_qc * ld_s;          // [DEC_VCH][32]
+    float* sR = sV + DEC_VCH * 32;            // per query: max, uniform flag, Σe, pad
+    float* sC = sR + 4 * ATT_DEC_MAX_Q;       // [qc][32]
+    __shared__ float wred[4][ATT_DEC_MAX_Q];
+    __shared__ int wnan[4][ATT_DEC_MAX_Q];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD + 32 * sl;
+
+    // V chunk c: float4 e = tid + 256j is key e / 8, dimensions 4(e % 8) .. +3 of the slice
+    v4f vr[8];
+    auto vload = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int e = tid + 256 * j;
+            const int key = min(c * DEC_VCH + (e >> 3), nk - 1);
+            vr[j] = *reinterpret_cast<const v4f*>(vb + (int64_t)key * ATT_HD + 4 * (e & 7));
+        }
+    };
+    vload(0);
+
+    const float* sc = scratch + it.s_off + (int64_t)head * qc * ld_k;
+    for (int qi = 0; qi < qc; qi++)
+        for (int key = tid; key < ld_s; key += 256)
+            sW[qi * ld_s + key] = key <= it.pos0 + qi ? sc[(int64_t)qi * ld_k + key] : 0.0f;
+    __syncthreads();
+
+    // row maxima (NaN noted: Kernels.Softmax then weighs every key equally)
+    for (int qi = 0; qi < qc; qi++) {
+        const int nq = it.pos0 + qi + 1;
+        float mx = -INFINITY;
+        int nan = 0;
+        for (int key = tid; key < nq; key += 256) {
+            const float v = sW[qi * ld_s + key];
+            mx = fmaxf(mx, v);
+            nan |= v != v;
+        }
+        mx = wave_max(mx);
+        nan = wave_or(nan);
+        if (lane == 0) {
+            wred[wave][qi] = mx;
+            wnan[wave][qi] = nan;
+        }
+    }
+    __syncthreads();
+    if (tid < qc) {
+        const float mx = fmaxf(fmaxf(wred[0][tid], wred[1][tid]), fmaxf(wred[2][tid], wred[3][tid]));
+        const int nan = wnan[0][tid] | wnan[1][tid] | wnan[2][tid] | wnan[3][tid];
+        sR[4 * tid] = mx;
+        sR[4 * tid + 1] = (nan || !(fabsf(mx) <= 3.402823466e38f)) ? 1.0f : 0.0f;
+    }
+    __syncthreads();
+
+    // e in place (keys of the row only; the rest stay 0)
+    for (int qi = 0; qi < qc; qi++) {
+        const float mx = sR[4 * qi];
+        const bool uniform = sR[4 * qi + 1] != 0.0f;
+        for (int key = tid; key <= it.pos0 + qi; key += 256)
+            sW[qi * ld_s + key] = uniform ? 1.0f : det_expf(sW[qi * ld_s + key] - mx);
+    }
+    __syncthreads();
+
+    // Σe: lane t of the 8-lane group of query qi sums residue t up to n8 in key order
+    if (tid < 8 * qc) {
+        const int qi = tid >> 3, t = tid & 7;
+        const int nq = it.pos0 + qi + 1, n8 = nq & ~7;
+        const float* e = sW + qi * ld_s;
+        float part = 0.0f;
+        int key = t;
+        for (; key + 56 < n8; key += 64) {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = e[key + 8 * k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) part = part + v[k];
+        }
+        for (; key < n8; key += 8) part = part + e[key];
+        float total = vsum8_lanes(part);
+        // the tail keys n8 .. nq − 1 in order (at most 7; read together, slots past nq are 0)
+        float tl[7];
+#pragma unroll
+        for (int k = 0; k < 7; k++) tl[k] = e[n8 + k];
+#pragma unroll
+        for (int k = 0; k < 7; k++) total = n8 + k < nq ? total + tl[k] : total;
+        if (t == 0) sR[4 * qi + 2] = total;
+    }
+    __syncthreads();
+
+    // w = e / Σe over the row's keys (the zeros past it stay), and the first V chunk into the LDS
+    for (int qi = 0; qi < qc; qi++) {
+        const float total = sR[4 * qi + 2];
+        for (int key = tid; key <= it.pos0 + qi; key += 256) sW[qi * ld_s + key] = sW[qi * ld_s + key] / total;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int e = tid + 256 * j;
+        *reinterpret_cast<v4f*>(sV + (e >> 3) * 32 + 4 * (e & 7)) = vr[j];
+    }
+
+    // values: lane (qi, d) runs the ordered chain over the keys; V staged per 256-key chunk.
+    // Steps past a query's last key have v = 0 and w = 0, so fma leaves ctx unchanged (ctx
+    // is never −0: it starts at +0 and a sum that cancels rounds to +0).
+    const int n_ch = (nk + DEC_VCH - 1) / DEC_VCH;
+    const int qi = tid >> 5, d = tid & 31;
+    const bool chain = tid < 32 * qc;
+    const int nq = it.pos0 + (chain ? qi : 0) + 1;
+    const float* w = sW + (chain ? qi : 0) * ld_s;
+    float acc = 0.0f;
+    for (int c = 0; c < n_ch; c++) {
+        if (c > 0) {
+            __syncthreads();  // the previous chunk's readers are done
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int e = tid + 256 * j;
+                *reinterpret_cast<v4f*>(sV + (e >> 3) * 32 + 4 * (e & 7)) = vr[j];
+            }
+        }
+        __syncthreads();
+        if (c + 1 < n_ch) vload(c + 1);
+        if (chain) {
+            const int k0 = c * DEC_VCH, k1 = min(k0 + DEC_VCH, nq);
+            // 16 steps at a time: weights as four float4 reads, then the chain; the chunk's rows
+            // are all staged (clamped past the last key), and only the last group masks its
+            // steps past k1
+            auto group = [&](int key, bool masked) {
+                float v[16];
+                float4 w4[4];
+#pragma unroll
+                for (int g = 0; g < 4; g++) w4[g] = *reinterpret_cast<const float4*>(w + key + 4 * g);
+#pragma unroll
+                for (int k = 0; k < 16; k++) v[k] = sV[(key - k0 + k) * 32 + d];
+                if (masked) {
+#pragma unroll
+                    for (int k = 0; k < 16; k++) v[k] = key + k < k1 ? v[k] : 0.0f;
+                }
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    acc = fmaf(v[4 * g], w4[g].x, acc);
+                    acc = fmaf(v[4 * g + 1], w4[g].y, acc);
+                    acc = fmaf(v[4 * g + 2], w4[g].z, acc);
+                    acc = fmaf(v[4 * g + 3], w4[g].w, acc);
+                }
+            };
+            const int kfull = k0 + ((k1 - k0) & ~15);
+            int key = k0;
+            for (; key < kfull; key += 16) group(key, false);
+            if (key < k1) group(key, true);
+        }
+    }
+    if (!ao.q) {
+        if (chain) ctx[(int64_t)(it.q_start + qi) * ldc + head * ATT_HD + 32 * sl + d] = acc;
+        return;
+    }
+    if (chain) sC[tid] = acc;
+    __syncthreads();
+    // the o projection's codes: 8 lanes per query, 4 dimensions each
+    if (tid < 8 * qc) {
+        const int q8 = tid >> 3, l8 = tid & 7;
+        const float4 v = *reinterpret_cast<const float4*>(sC + q8 * 32 + 4 * l8);
+        quant_block8(v, l8, ao, it.q_start + q8, (head * ATT_HD + 32 * sl) / 32, 0);
+    }
+}
+
+static size_t dec_scores_lds(int G, int max_qc)
+{
+    return sizeof(float) * ((size_t)DEC_KT * DEC_KROW + (size_t)G * max_qc * ATT_HD);
+}
+
+static size_t dec_pv_lds(int max_qc, int ld_s)
+{
+    return sizeof(float) * ((size_t)max_qc * ld_s + (size_t)DEC_VCH * 32 + 4 * ATT_DEC_MAX_Q + (size_t)max_qc * 32);
+}
+
+int attn_decode_max_keys(int max_qc, int max_lds_bytes)
+{
+    if (max_qc < 1 || max_qc > ATT_DEC_MAX_Q) return 0;
+    const int64_t room = (int64_t)max_lds_bytes - (int64_t)dec_pv_lds(max_qc, 0) - 1024;
+    // a row's stride is the key count rounded up by at most 15
+    const int64_t keys = room / (int64_t)sizeof(float) / max_qc - 15;
+    return keys > 0 ? (int)keys : 0;
+}
+
+hipError_t launch_attn_decode(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
+                              int n_items, int n_head, int n_kv, int head_dim, float scale, int max_qc, int max_keys,
+                              float* scratch, float* ctx, int ldc, const ActQ8* codes, hipStream_t s)
+{
+    if (head_dim != ATT_HD || n_kv <= 0 || n_head % n_kv != 0 || n_head / n_kv > 4 || max_qc < 1 ||
+        max_qc > ATT_DEC_MAX_Q)
+        return hipErrorInvalidValue;
+    if (n_items <= 0) return hipSuccess;
+    const int G = n_head / n_kv;
+    const int n_chunks = (max_keys + DEC_KT - 1) / DEC_KT;
+    const size_t shs = dec_scores_lds(G, max_qc);
+    if (shs > (64u << 10)) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_dec_scores),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)shs);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k_attn_dec_scores, dim3((unsigned)(n_items * n_kv * n_chunks)), dim3(256), shs, s, q, ldq, kc,
+                       cap, items, n_head, n_kv, n_chunks, scale, scratch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int ld_s = (max_keys + 15) & ~15;  // the value loop reads weights 16 at a time
+    const size_t shp = dec_pv_lds(max_qc, ld_s);
+    if (shp > (64u << 10)) {
+        e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_dec_pv), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)shp);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(k_attn_dec_pv, dim3((unsigned)(n_items * n_head * (ATT_HD / 32))), dim3(256), shp, s, vc, cap,
+                       items, n_head, n_kv, ld_s, max_qc, scratch, ctx, ldc, codes ? *codes : ActQ8());
     return hipGetLastError();
 }
 

@@ -96,8 +96,33 @@ def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
             g = gpu.forward_selected(toks, ids)
             o = ora.forward(toks, head_mode=1, vocab_ids=ids)
             assert np.array_equal(g, o), (n, H.rel_l2(g, o))
+        # decode width onto the 1100-token cache: 2 queries, then 1 (k_attn_decode)
+        gpu.profile(True)
+        gpu.profile_reset()
+        try:
+            for step in (rng.integers(0, cfg.vocab, 2), rng.integers(0, cfg.vocab, 1)):
+                g = gpu.forward(step)
+                o = ora.forward(step, head_mode=2)
+                assert np.array_equal(g, o), H.rel_l2(g, o)
+            assert gpu.profile_read("k_attn_decode")[0] == 2 * cfg.n_layer
+        finally:
+            gpu.profile(False)
     finally:
         gpu.close()
+
+
+def test_packed_batch_of_decode_width_prompts_matches_the_oracle(shs, oracle, tiny):
+    """A packed batch of 1-4-token prompts: every item is decode width, so attention runs
+    k_attn_decode over 5 items and the GEMMs the narrow kernel (T = 12 > 4 takes k_gemm:
+    both widths meet in one model)."""
+    cfg, tensors, types, gpu, ora = tiny
+    rng = np.random.default_rng(19)
+    prompts = [rng.integers(0, cfg.vocab, n) for n in (1, 4, 2, 3, 2)]
+    ids = [5, 6, 500]
+    batch = gpu.forward_batch(prompts, ids)
+    for p, row in zip(prompts, batch):
+        ora.reset()
+        assert np.array_equal(row, ora.forward(p, head_mode=1, vocab_ids=ids))
 
 
 def test_selected_rows_are_bit_identical_to_the_full_head(shs, tiny):
