@@ -7,6 +7,9 @@ compute the Score on the host (ShieldstralModerator.ModerateAsync without tokeni
 Weights are a random-init model of the real architecture built in HBM (synthetic data);
 token ids are uniform over the vocabulary. Single GPU only.
 
+With --decode the step is instead one single-token forward with full-vocabulary logits onto
+a 256-token context (the shape Benchmark.BenchmarkModel's decode runs, Benchmark.cs:399-410).
+
 Prints one JSON line; see --help for options.
 """
 import argparse
@@ -86,15 +89,7 @@ def cpu_baseline(model, cfg, tokens, ids, gpu_logits):
     import numpy as np
     import oracle as O
 
-    full = O.make_config(n_layer=cfg.layer_count, hidden=cfg.hidden_size, n_head=cfg.head_count,
-                         n_kv_head=cfg.kv_head_count, head_dim=cfg.head_dim, ffn=cfg.feed_forward_size,
-                         vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_theta=cfg.rope_freq_base,
-                         rope_dim=cfg.rope_dim, rope_scale=cfg.rope_scale_factor,
-                         rope_orig_ctx=cfg.rope_original_context_length, yarn_beta_fast=cfg.yarn_beta_fast,
-                         yarn_beta_slow=cfg.yarn_beta_slow, yarn_ext_factor=cfg.yarn_ext_factor,
-                         yarn_mscale=cfg.yarn_mscale, yarn_mscale_all_dim=cfg.yarn_mscale_all_dim,
-                         rope_attn_factor=cfg.rope_attn_factor, attn_temperature=cfg.attention_temperature_scale,
-                         yarn_active=int(cfg.yarn_active))
+    full = oracle_config(O, cfg)
     names = list(cfg.tensor_shapes(2, 2))
     tensors = {n: model.download(n) for n in names}
     types = {n: (0 if n.endswith("norm.weight") else 2) for n in names}
@@ -112,6 +107,129 @@ def cpu_baseline(model, cfg, tokens, ids, gpu_logits):
                                                               np.asarray(gpu_logits, np.float32).view(np.uint32)))}
 
 
+def oracle_config(O, cfg):
+    return O.make_config(n_layer=cfg.layer_count, hidden=cfg.hidden_size, n_head=cfg.head_count,
+                         n_kv_head=cfg.kv_head_count, head_dim=cfg.head_dim, ffn=cfg.feed_forward_size,
+                         vocab=cfg.vocab_size, eps=cfg.rms_norm_eps, rope_theta=cfg.rope_freq_base,
+                         rope_dim=cfg.rope_dim, rope_scale=cfg.rope_scale_factor,
+                         rope_orig_ctx=cfg.rope_original_context_length, yarn_beta_fast=cfg.yarn_beta_fast,
+                         yarn_beta_slow=cfg.yarn_beta_slow, yarn_ext_factor=cfg.yarn_ext_factor,
+                         yarn_mscale=cfg.yarn_mscale, yarn_mscale_all_dim=cfg.yarn_mscale_all_dim,
+                         rope_attn_factor=cfg.rope_attn_factor, attn_temperature=cfg.attention_temperature_scale,
+                         yarn_active=int(cfg.yarn_active))
+
+
+DECODE_CONTEXT = 256
+DECODE_METRIC = "decode tok/s (single-token forwards, full-vocabulary logits, 256-token context), Shieldstral-3B Q4_0, 1 MI355X"
+
+
+def decode_main(args):
+    """Decode: prefill 255 prompt tokens (untimed), then K single-token forwards, each returning
+    the full 131072-entry logits row to the host like MinistralModel.ForwardAsync. The timed
+    region is the K forwards; the context grows from 256 to 256 + K − 1 keys."""
+    import numpy as np
+    import shieldstral as S
+
+    cfg = S.SHIELDSTRAL_3B
+    S.load_library()
+    P = DECODE_CONTEXT
+    model = S.MinistralModel.synthetic(cfg, S.Q4_0, seed=args.seed, initial_cache_capacity=P + args.steps + 8)
+    rng = np.random.default_rng(args.seed)
+    prompt = rng.integers(0, cfg.vocab_size, P).astype(np.int32)
+    steps = rng.integers(0, cfg.vocab_size, args.steps).astype(np.int32)
+
+    def run():
+        model.reset_kv_cache()
+        model.prefill(prompt[:-1])
+        model.synchronize()
+        out = [model.forward(prompt[-1:])]
+        t0 = time.perf_counter()
+        for tok in steps:
+            out.append(model.forward(np.array([tok], np.int32)))
+        model.synchronize()
+        return time.perf_counter() - t0, out
+
+    for _ in range(max(args.warmup, 1)):
+        run()
+    elapsed, logits = run()
+    ms = elapsed / args.steps * 1e3
+    # per-kernel timing: the same forwards again with HIP events around every launch
+    model.reset_kv_cache()
+    model.prefill(prompt[:-1])
+    model.forward(prompt[-1:])
+    model.synchronize()
+    model.profile_reset()
+    model.profile(True)
+    for tok in steps:
+        model.forward(np.array([tok], np.int32))
+    model.synchronize()
+    model.profile(False)
+    breakdown = {}
+    for cls in ["gemm*", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "gemm_head", "attention", "rmsnorm_quant",
+                "rope_store", "swiglu_quant", "embed"]:
+        c, cms, _ = model.profile_read(cls)
+        if c:
+            breakdown[cls.rstrip("*") + ("_all" if cls.endswith("*") else "")] = {
+                "launches_per_step": c // args.steps, "ms_per_step": round(cms / args.steps, 4),
+                "us_per_launch": round(cms / c * 1e3, 2)}
+    # Roofline: the narrow GEMM of the layer projections streams each weight matrix once;
+    # algorithmic bytes per token and layer = the repacked Q4_0 weights (16 B of codes and a
+    # 4-byte fp32 scale per 32-weight block) of q|k|v, o, gate|up and down.
+    h, q, kv, f = cfg.hidden_size, cfg.q_dim, cfg.kv_dim, cfg.feed_forward_size
+    blocks = ((q + 2 * kv) * h + q * h + 2 * f * h + f * h) // 32
+    layer_bytes = blocks * 20
+    g_ms = sum(model.profile_read(c)[1] for c in ("gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down"))
+    achieved = layer_bytes * cfg.layer_count * args.steps / (g_ms * 1e-3) / 1e9 if g_ms > 0 else 0.0
+    line = {
+        "metric": DECODE_METRIC,
+        "value": round(args.steps / elapsed, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"Shieldstral-3B-shaped random-init Q4_0 model, {args.steps} single-token forwards "
+                               f"with full-vocabulary logits onto a {P}-token context",
+                   "layers": cfg.layer_count, "hidden": h, "ffn": f, "vocab": cfg.vocab_size, "context": P,
+                   "weights": "Q4_0", "seed": args.seed},
+        "roofline": {"bound": "hbm",
+                     "kernel": "k_gemm_narrow (q|k|v, o, gate|up, down at one token): Q4_0 weights streamed once",
+                     "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_token_and_layer": layer_bytes},
+        "breakdown": breakdown,
+    }
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import oracle as O
+        names = list(cfg.tensor_shapes(2, 2))
+        tensors = {n: model.download(n) for n in names}
+        types = {n: (0 if n.endswith("norm.weight") else 2) for n in names}
+        om = O.OracleModel(oracle_config(O, cfg), tensors, types, cap=P + args.steps + 8)
+        threads = os.cpu_count() or 1
+        om.forward(prompt, head_mode=0, threads=threads)
+        n_cpu = min(4, args.steps)
+        same = True
+        t0 = time.perf_counter()
+        for i in range(n_cpu):
+            o = om.forward(steps[i:i + 1], head_mode=2, threads=threads)
+            same = same and bool(np.array_equal(np.asarray(o, np.float32).view(np.uint32),
+                                                np.asarray(logits[i + 1], np.float32).view(np.uint32)))
+        cpu_s = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(n_cpu / cpu_s, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                                "sample": f"oracle decode of the first {n_cpu} of the same single-token forwards "
+                                          f"(full head) after the same {P}-token prompt; {cpu_s:.1f} s",
+                                "logits_bit_identical_to_gpu": same}
+    model.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -124,11 +242,15 @@ def main():
                     help="time without the per-kernel HIP events (no roofline or breakdown)")
     ap.add_argument("--copy-probe", action="store_true",
                     help=f"first copy {COPY_PROBE_BYTES >> 20} MiB device to device (counter calibration)")
+    ap.add_argument("--decode", action="store_true",
+                    help=f"measure decode instead: --steps single-token forwards onto a {DECODE_CONTEXT}-token context")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the verdict path does not shard "
               f"across GPUs in this build.", file=sys.stderr)
         return 2
+    if args.decode:
+        return decode_main(args)
 
     import numpy as np
     import shieldstral as S

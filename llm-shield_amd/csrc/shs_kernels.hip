@@ -1183,10 +1183,11 @@ static size_t narrow_lds_bytes(int R, int B, int nt, bool off)
     return 32 * (size_t)nt * B + 8 * (size_t)nt * R * pb + (off ? 4 * (size_t)R * pb : 0) + 4 * (size_t)nt * B * 3;
 }
 
-// Rows per work-group: 8 for the layer projections (many work-groups for a few MB of
-// weights), 32 for matrices of 64k rows and more (the vocabulary head: one tile per
-// work-group, its activation staging spread over 4× the weights).
-static int narrow_rows(const DevMatrix& w) { return w.rows >= 65536 ? 32 : 8; }
+// Rows per work-group: 8 for the smaller layer projections (many work-groups for a few MB of
+// weights), 16 from 16k rows (gate|up: its work-groups then fit the device at once), 32 from
+// 64k rows (the vocabulary head: one tile per work-group, its activation staging spread over
+// 4× the weights).
+static int narrow_rows(const DevMatrix& w) { return w.rows >= 65536 ? 32 : w.rows >= 16384 ? 16 : 8; }
 
 // One batch of a thread's row-blocks: blocks b0 + j·(256/R), j < 4, clamped to the last
 // block (a clamped load re-reads a line the work-group already has).
@@ -1279,8 +1280,12 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     }
     __syncthreads();
 
-    for (int b0 = bl; b0 < B; b0 += 4 * BS) {
-        narrow_load<TYPE, R>(nxt, wqs, wqh, wd, wm, rec0, ri, min(b0 + 4 * BS, B - 1), B);
+    // batches of 4·BS blocks; the next batch is prefetched only when there is one (a barrier
+    // waits for every load in flight)
+    const int n_batch = (B + 4 * BS - 1) / (4 * BS);
+    for (int bt = 0; bt < n_batch; bt++) {
+        const int b0 = bl + bt * 4 * BS;
+        if (bt + 1 < n_batch) narrow_load<TYPE, R>(nxt, wqs, wqh, wd, wm, rec0, ri, b0 + 4 * BS, B);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int b = b0 + j * BS;
@@ -1307,7 +1312,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
                 }
             }
         }
-        cur = nxt;
+        if (bt + 1 < n_batch) cur = nxt;
     }
     __syncthreads();
 
@@ -1369,8 +1374,11 @@ static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, in
 template <int TYPE, int NT, int MODE>
 static hipError_t narrow_rows_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
 {
-    return narrow_rows(w) == 32 ? narrow_launch<TYPE, NT, MODE, 32>(w, a, y, ldy, s)
-                                : narrow_launch<TYPE, NT, MODE, 8>(w, a, y, ldy, s);
+    switch (narrow_rows(w)) {
+    case 32: return narrow_launch<TYPE, NT, MODE, 32>(w, a, y, ldy, s);
+    case 16: return narrow_launch<TYPE, NT, MODE, 16>(w, a, y, ldy, s);
+    default: return narrow_launch<TYPE, NT, MODE, 8>(w, a, y, ldy, s);
+    }
 }
 
 template <int TYPE, int MODE>
