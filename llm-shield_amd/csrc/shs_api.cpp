@@ -894,18 +894,22 @@ double gemm_ops(int T, const DevMatrix& w) { return 2.0 * T * (double)w.rows * w
 
 // Each launch is timed under the projection's class and under its kernel instantiation,
 // "k_gemm<type,TT,mode>" (the name rocprofv3 reports, so the two can be compared).
+// The name rocprofv3 reports for the GEMM kernel launch_gemm* picks for this shape and mode.
+void gemm_kname(char* buf, size_t n, const DevMatrix& w, const ActQ8& a, int mode)
+{
+    const int nt = gemm_narrow_tokens(w, a, mode);
+    if (nt > 0)
+        snprintf(buf, n, "k_gemm_narrow<%d,%d,%d>", w.type, nt, mode);
+    else
+        snprintf(buf, n, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, a, mode), mode);
+}
+
 shs_status run_proj(shs_model* m, const Proj& p, const ActQ8& a, float* y, int ldy, int mode, const char* cls)
 {
     for (size_t i = 0; i < p.parts.size(); i++) {
         const DevMatrix& w = p.parts[i];
         char kname[48] = "k_gemm";
-        if (m->prof.on) {
-            const int nt = gemm_narrow_tokens(w, a);
-            if (nt > 0 && (mode == GEMM_STORE || mode == GEMM_ADD))
-                snprintf(kname, sizeof kname, "k_gemm_narrow<%d,%d,%d>", w.type, nt, mode);
-            else
-                snprintf(kname, sizeof kname, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, a, mode), mode);
-        }
+        if (m->prof.on) gemm_kname(kname, sizeof kname, w, a, mode);
         Timed tm(m->prof, cls, gemm_ops(a.T, w), m->stream, kname);
         HIP_TRY(launch_gemm(w, a, y + p.col0[i], ldy, mode, m->stream));
     }
@@ -969,7 +973,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         snprintf(name, sizeof name, "blk.%d.attn_norm", l);
         if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
 
-        if (!cap_on && L.qkv.parts.size() == 1 && c.head_dim % 32 == 0 && gemm_narrow_tokens(L.qkv.parts[0], ah) == 0) {
+        if (!cap_on && L.qkv.parts.size() == 1 && c.head_dim % 32 == 0) {
             // one fused matrix: RoPE and the KV-cache store in the epilogue
             RopeArgs ra;
             ra.pos = m->pos.as<int32_t>();
@@ -986,8 +990,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             ra.slot0 = slot0;
             const DevMatrix& w = L.qkv.parts[0];
             char kname[48] = "k_gemm";
-            if (m->prof.on)
-                snprintf(kname, sizeof kname, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, ah, GEMM_QKV), GEMM_QKV);
+            if (m->prof.on) gemm_kname(kname, sizeof kname, w, ah, GEMM_QKV);
             Timed tm(m->prof, "gemm_qkv", gemm_ops(T, w), m->stream, kname);
             HIP_TRY(launch_gemm_qkv(w, ah, qkv, ldqkv, ra, m->stream));
         } else {
@@ -1075,13 +1078,12 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         ActQ8 af = a;
         af.K = c.ffn;
         af.B = c.ffn / 32;
-        if (!cap_on && L.gu.parts.size() == 1 && gemm_narrow_tokens(L.gu.parts[0], ah) == 0) {
+        if (!cap_on && L.gu.parts.size() == 1) {
             // one fused matrix: SwiGLU and the down projection's quantization in the epilogue
             HIP_TRY(m->act_ffn.ensure(T, c.ffn, &af));
             const DevMatrix& w = L.gu.parts[0];
             char kname[48] = "k_gemm";
-            if (m->prof.on)
-                snprintf(kname, sizeof kname, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, ah, GEMM_SWIGLU), GEMM_SWIGLU);
+            if (m->prof.on) gemm_kname(kname, sizeof kname, w, ah, GEMM_SWIGLU);
             Timed tm(m->prof, "gemm_gate_up", gemm_ops(T, w), m->stream, kname);
             HIP_TRY(launch_gemm_swiglu(w, ah, c.ffn / 32, af, m->stream));
         } else {

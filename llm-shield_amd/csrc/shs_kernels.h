@@ -98,11 +98,11 @@ hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, cons
 hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s);
 // The token tiles per block launch_gemm picks for this shape (the k_gemm instantiation's TT).
 int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode);
-// Up to NARROW_MAX_T tokens, launch_gemm (store and add) streams the weights through
-// k_gemm_narrow instead; returns the token count when it does, else 0. The fused q|k|v and
-// gate|up launchers always take k_gemm.
+// Up to NARROW_MAX_T tokens, launch_gemm, launch_gemm_qkv and launch_gemm_swiglu stream the
+// weights through k_gemm_narrow instead (same epilogues); returns the token count when they
+// do for this mode, else 0.
 enum { NARROW_MAX_T = 4 };
-int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a);
+int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a, int mode);
 hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* out, hipStream_t s);
 hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* row_ids, int n_ids, float* y,
                             hipStream_t s);

@@ -278,32 +278,38 @@ __device__ inline float vsum8(const float* a)
 
 // Kernels.RmsNorm (Kernels.cs:26-61) in its own order — 16 running float sums of x²
 // (8 "even" lanes, 8 "odd" lanes of Vector<float>), each pairwise-summed and widened to
-// double — followed by y = (x·s)·w and the 32-block quantization of y. One block per token.
-__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x, int ldx,
-                                                       const float* __restrict__ w, float eps, int n,
-                                                       ActQ8 a, float* __restrict__ y_opt)
+// double — followed by y = (x·s)·w and the 32-block quantization of y: token t's row xr,
+// by a whole block of 256 threads. LDS: sx holds 2n floats (the row, then its squares),
+// part 16 floats and s_scale one. Ends with the block's threads past a barrier only if the
+// caller adds one (the next use of sx must be preceded by __syncthreads()).
+__device__ __forceinline__ void rmsnorm_quant_token(const float* __restrict__ xr, const float* __restrict__ w,
+                                                    float eps, int n, const ActQ8& a, int t,
+                                                    float* __restrict__ y_row, float* sx, float* part,
+                                                    float* s_scale)
 {
-    extern __shared__ float sx[];  // the row, then its squares
-    __shared__ float part[16];
-    __shared__ float s_scale;
-    const int t = blockIdx.x, tid = threadIdx.x;
-    if (t >= a.T) {
-        for (int b = tid >> 3; b < a.B; b += blockDim.x >> 3) zero_block8(tid & 7, a, t, b);
-        return;
-    }
-    const float* xr = x + (int64_t)t * ldx;
+    const int tid = threadIdx.x;
     float* sq = sx + n;
+    // the gains this thread's 8-lane group applies (blocks tid/8 + 32i, 4 elements each),
+    // loaded now so their latency overlaps the row's
+    constexpr int WPRE = 4;
+    float4 wpre[WPRE];
+    const int l8 = tid & 7;
+#pragma unroll
+    for (int i = 0; i < WPRE; i++) {
+        const int b = (tid >> 3) + (256 >> 3) * i;
+        wpre[i] = b < a.B ? *reinterpret_cast<const float4*>(w + 32 * b + 4 * l8) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     if (((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (n & 3) == 0) {
         // float4 row copy, the loads of a thread issued together; the squares x·x (rounded,
         // as the reference's running sums add them) alongside
 #pragma unroll 4
-        for (int i = tid; i < n / 4; i += blockDim.x) {
+        for (int i = tid; i < n / 4; i += 256) {
             const float4 v = reinterpret_cast<const float4*>(xr)[i];
             reinterpret_cast<float4*>(sx)[i] = v;
             reinterpret_cast<float4*>(sq)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
         }
     } else {
-        for (int i = tid; i < n; i += blockDim.x) {
+        for (int i = tid; i < n; i += 256) {
             const float v = xr[i];
             sx[i] = v;
             sq[i] = v * v;
@@ -335,23 +341,46 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
             i = n / 16 * 16;
         }
         for (; i < n; i++) sum += (double)sx[i] * (double)sx[i];
-        s_scale = 1.0f / sqrtf((float)(sum / n) + eps);
+        *s_scale = 1.0f / sqrtf((float)(sum / n) + eps);
     }
     __syncthreads();
-    const float sc = s_scale;
-    const int l8 = tid & 7;
-    for (int b = tid >> 3; b < a.B; b += blockDim.x >> 3) {  // uniform per 8-lane group
+    const float sc = *s_scale;
+    int i = 0;
+    for (int b = tid >> 3; b < a.B; b += 256 >> 3, i++) {  // uniform per 8-lane group
         const int e = 32 * b + 4 * l8;
         const float4 xv = *reinterpret_cast<const float4*>(sx + e);
-        const float4 wv = *reinterpret_cast<const float4*>(w + e);
+        float4 wv;
+        if (i < WPRE) {
+            // (a register array read with a runtime index would go to scratch: select instead)
+            wv = i == 0 ? wpre[0] : i == 1 ? wpre[1] : i == 2 ? wpre[2] : wpre[3];
+        } else {
+            wv = *reinterpret_cast<const float4*>(w + e);
+        }
         float4 v;
         v.x = (xv.x * sc) * wv.x;
         v.y = (xv.y * sc) * wv.y;
         v.z = (xv.z * sc) * wv.z;
         v.w = (xv.w * sc) * wv.w;
-        if (y_opt) *reinterpret_cast<float4*>(y_opt + (int64_t)t * n + e) = v;
+        if (y_row) *reinterpret_cast<float4*>(y_row + e) = v;
         quant_block8(v, l8, a, t, b, 0);
     }
+}
+
+// One block of 256 threads per token (padding tokens get zero codes).
+__global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x, int ldx,
+                                                       const float* __restrict__ w, float eps, int n,
+                                                       ActQ8 a, float* __restrict__ y_opt)
+{
+    extern __shared__ float sx[];  // the row, then its squares
+    __shared__ float part[16];
+    __shared__ float s_scale;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (t >= a.T) {
+        for (int b = tid >> 3; b < a.B; b += blockDim.x >> 3) zero_block8(tid & 7, a, t, b);
+        return;
+    }
+    rmsnorm_quant_token(x + (int64_t)t * ldx, w, eps, n, a, t, y_opt ? y_opt + (int64_t)t * n : nullptr, sx, part,
+                        &s_scale);
 }
 
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float eps, int n, const ActQ8& a,
@@ -901,6 +930,9 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     }
 }
 
+static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s,
+                                     const ActQ8& ao, int n_ft, const RopeArgs& ra);
+
 template <int TYPE, int TT, int MODE>
 static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
                               const ActQ8& ao = ActQ8(), int n_ft = 0, const RopeArgs& ra = RopeArgs())
@@ -1000,6 +1032,8 @@ int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode)
 hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s)
 {
     if (w.tiles != 2 * n_ft || out.B != n_ft || out.Tpad != a.Tpad) return hipErrorInvalidValue;
+    if (gemm_narrow_tokens(w, a, GEMM_SWIGLU) > 0)
+        return launch_gemm_narrow(w, a, nullptr, 0, GEMM_SWIGLU, s, out, n_ft, RopeArgs());
     switch (w.type) {
     case SHS_TYPE_Q4_0: return gemm_swiglu_type<SHS_TYPE_Q4_0>(w, a, n_ft, out, s);
     case SHS_TYPE_Q4_1: return gemm_swiglu_type<SHS_TYPE_Q4_1>(w, a, n_ft, out, s);
@@ -1015,6 +1049,8 @@ hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy
     if (ra.hd % 32 != 0 || w.rows != (ra.n_head + 2 * ra.n_kv) * ra.hd || (ldy & 3) != 0 ||
         (reinterpret_cast<uintptr_t>(y) & 15) != 0)
         return hipErrorInvalidValue;
+    if (gemm_narrow_tokens(w, a, GEMM_QKV) > 0)
+        return launch_gemm_narrow(w, a, y, ldy, GEMM_QKV, s, ActQ8(), 0, ra);
     switch (w.type) {
     case SHS_TYPE_Q4_0: return gemm_qkv_type<SHS_TYPE_Q4_0>(w, a, y, ldy, ra, s);
     case SHS_TYPE_Q4_1: return gemm_qkv_type<SHS_TYPE_Q4_1>(w, a, y, ldy, ra, s);
@@ -1025,12 +1061,10 @@ hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy
     }
 }
 
-static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s);
-
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
 {
-    if ((mode == GEMM_STORE || mode == GEMM_ADD) && gemm_narrow_tokens(w, a) > 0)
-        return launch_gemm_narrow(w, a, y, ldy, mode, s);
+    if ((mode == GEMM_STORE || mode == GEMM_ADD) && gemm_narrow_tokens(w, a, mode) > 0)
+        return launch_gemm_narrow(w, a, y, ldy, mode, s, ActQ8(), 0, RopeArgs());
     switch (w.type) {
     case SHS_TYPE_Q4_0: return gemm_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s);
     case SHS_TYPE_Q4_1: return gemm_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s);
@@ -1174,6 +1208,19 @@ hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* i
 
 // ------------------------------------------------- narrow GEMM (decode, T ≤ 4)
 
+// Rows per work-group (R): 8 for the smaller layer projections (many work-groups for a few MB
+// of weights), 16 from 16k rows, 32 from 64k rows (the vocabulary head: one tile per
+// work-group, its activation staging spread over 4× the weights); the fused gate|up takes a
+// gate tile and its up tile (64 rows), so a work-group owns whole 32-feature blocks.
+static int narrow_rows(const DevMatrix& w, int mode)
+{
+    if (mode == GEMM_SWIGLU) return 64;
+    return w.rows >= 65536 ? 32 : w.rows >= 16384 ? 16 : 8;
+}
+
+// Row-blocks per batch and thread: 8 when a thread owns many blocks (64-row work-groups).
+__host__ __device__ constexpr int narrow_nb(int R) { return R >= 64 ? 8 : 4; }
+
 // Bytes of dynamic LDS k_gemm_narrow<.., R> needs for B blocks and nt tokens: the activation
 // codes, then per (token, row, block) the pair (I, RN(d_w·d_a)), then m_w per (row, block)
 // for the offset types, then Σa, d_a and RN(d_a·Σa) per (token, block).
@@ -1183,28 +1230,22 @@ static size_t narrow_lds_bytes(int R, int B, int nt, bool off)
     return 32 * (size_t)nt * B + 8 * (size_t)nt * R * pb + (off ? 4 * (size_t)R * pb : 0) + 4 * (size_t)nt * B * 3;
 }
 
-// Rows per work-group: 8 for the smaller layer projections (many work-groups for a few MB of
-// weights), 16 from 16k rows (gate|up: its work-groups then fit the device at once), 32 from
-// 64k rows (the vocabulary head: one tile per work-group, its activation staging spread over
-// 4× the weights).
-static int narrow_rows(const DevMatrix& w) { return w.rows >= 65536 ? 32 : w.rows >= 16384 ? 16 : 8; }
-
-// One batch of a thread's row-blocks: blocks b0 + j·(256/R), j < 4, clamped to the last
+// One batch of a thread's row-blocks: blocks b0 + j·(256/R), j < NB, clamped to the last
 // block (a clamped load re-reads a line the work-group already has).
-template <int TYPE>
+template <int TYPE, int NB>
 struct NarrowBatch {
-    uint4 q[4], q8[4];
-    uint32_t qh[4];
-    float dw[4], mw[4];
+    uint4 q[NB], q8[NB];
+    uint32_t qh[NB];
+    float dw[NB], mw[NB];
 };
 
-template <int TYPE, int R>
-__device__ __forceinline__ void narrow_load(NarrowBatch<TYPE>& nb, const uint8_t* __restrict__ wqs,
+template <int TYPE, int R, int NB>
+__device__ __forceinline__ void narrow_load(NarrowBatch<TYPE, NB>& nb, const uint8_t* __restrict__ wqs,
                                             const uint32_t* __restrict__ wqh, const float* __restrict__ wd,
                                             const float* __restrict__ wm, int64_t rec0, int ri, int b0, int B)
 {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NB; ++j) {
         const int64_t rec = rec0 + min(b0 + j * (256 / R), B - 1);
         if (TYPE == SHS_TYPE_Q8_0) {
             nb.q[j] = *reinterpret_cast<const uint4*>(wqs + rec * 1024 + ri * 32);
@@ -1218,30 +1259,36 @@ __device__ __forceinline__ void narrow_load(NarrowBatch<TYPE>& nb, const uint8_t
     }
 }
 
-// y = x·Wᵀ (mode 0 store, 1 add into y) for NT ≤ 4 tokens: single-token decode and the
-// full-vocabulary head at the last position. At this width the weights are streamed once
-// from HBM and the int8 MFMA's 32-token tiles would be mostly padding, so a work-group takes
-// R rows × all blocks:
+// y = x·Wᵀ for NT ≤ 4 tokens: single-token decode and the full-vocabulary head at the last
+// position. At this width the weights are streamed once from HBM and the int8 MFMA's
+// 32-token tiles would be mostly padding, so a work-group takes R rows × all blocks:
 // - the first batch of weight loads is issued, then the activation codes, d_a, Σa (from the
 //   conversion column) and RN(d_a·Σa) are staged in the LDS under its latency;
-// - phase 1: thread (row r = tid % R, blocks b ≡ tid / R mod 256/R, four per batch, the next
+// - phase 1: thread (row r = tid % R, blocks b ≡ tid / R mod 256/R, NB per batch, the next
 //   batch loading while this one computes) forms the exact block sums I = Σu·a − z·Σa of
 //   every token with v_dot4 and the scale RN(d_w·d_a) into the LDS;
 // - phase 2: lane (t, r) runs the reference's chain acc = fma(I_b, RN(d_w·d_a), acc)
 //   [then fma(m_w, RN(d_a·Σa), acc) for the offset types] over b in order
 //   (IntegerGemm.cs:384-397) — k_gemm's arithmetic, so an output does not depend on the
-//   path that computed it.
+//   path that computed it;
+// - the epilogue by mode, as k_gemm's: 0 store, 1 add into y; 3 (q|k|v) RoPE on adjacent
+//   row pairs (neighbouring lanes), the query position scale, q into y and k, v into the KV
+//   cache; 2 (gate|up, work-group = gate tile f and up tile f) SwiGLU of each feature, then
+//   the 32-feature block quantized into the down projection's codes `ao`.
 // The grid is a multiple of 8 and work-group g of the logical order runs on XCD g / (grid/8):
 // the work-groups of a 32-row tile share its d (and qh, m) lines in one L2.
 template <int TYPE, int NT, int MODE, int R>
 __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                      const float* __restrict__ wd, const float* __restrict__ wm,
-                                                     int rows, int B, int n_wg, ActQ8 a, float* __restrict__ y, int ldy)
+                                                     int rows, int B, int n_wg, ActQ8 a, float* __restrict__ y, int ldy,
+                                                     ActQ8 ao, int n_ft, RopeArgs ra)
 {
     constexpr bool OFF = TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1;
     constexpr bool Q8 = TYPE == SHS_TYPE_Q8_0;
     constexpr int Z = ZeroPoint<TYPE>::z;
     constexpr int BS = 256 / R;  // block stride between a thread's row-blocks
+    constexpr int NB = narrow_nb(R);
+    static_assert(MODE != GEMM_SWIGLU || R == 64, "the gate|up epilogue pairs a gate tile with its up tile");
     const int g = (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
     if (g >= n_wg) return;
     extern __shared__ uint4 nw_lds[];
@@ -1254,12 +1301,17 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     float* sDs = sDa + NT * B;                                       // [NT][B] RN(d_a·Σa)
     const int tid = threadIdx.x;
     const int r = tid % R, bl = tid / R;
-    const int row = g * R + r;  // < tiles·32: n_wg covers the padded rows exactly
+    // the work-group's local row r: gate row 32g + r or up row 32(n_ft + g) + r − 32 (mode 2),
+    // else row gR + r (< tiles·32: n_wg covers the padded rows exactly)
+    auto global_row = [&](int lr) {
+        return MODE == GEMM_SWIGLU ? (lr < 32 ? 32 * g + lr : 32 * (n_ft + g) + lr - 32) : g * R + lr;
+    };
+    const int row = global_row(r);
     const int64_t rec0 = (int64_t)(row >> 5) * B;
     const int ri = row & 31;
 
-    NarrowBatch<TYPE> cur, nxt;
-    narrow_load<TYPE, R>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
+    NarrowBatch<TYPE, NB> cur, nxt;
+    narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
 
     for (int i = tid; i < NT * B * 2; i += 256) {
         const int t = i / (2 * B), rem = i - t * 2 * B, b = rem >> 1, h = rem & 1;
@@ -1280,14 +1332,14 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     }
     __syncthreads();
 
-    // batches of 4·BS blocks; the next batch is prefetched only when there is one (a barrier
+    // batches of NB·BS blocks; the next batch is prefetched only when there is one (a barrier
     // waits for every load in flight)
-    const int n_batch = (B + 4 * BS - 1) / (4 * BS);
+    const int n_batch = (B + NB * BS - 1) / (NB * BS);
     for (int bt = 0; bt < n_batch; bt++) {
-        const int b0 = bl + bt * 4 * BS;
-        if (bt + 1 < n_batch) narrow_load<TYPE, R>(nxt, wqs, wqh, wd, wm, rec0, ri, b0 + 4 * BS, B);
+        const int b0 = bl + bt * NB * BS;
+        if (bt + 1 < n_batch) narrow_load<TYPE, R, NB>(nxt, wqs, wqh, wd, wm, rec0, ri, b0 + NB * BS, B);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NB; ++j) {
             const int b = b0 + j * BS;
             if (b < B) {
                 const v4i w0 = Q8 ? v4i{(int)cur.q[j].x, (int)cur.q[j].y, (int)cur.q[j].z, (int)cur.q[j].w}
@@ -1316,19 +1368,20 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     }
     __syncthreads();
 
-    if (tid < NT * R) {
-        const int t = tid / R, rr = tid % R;
+    const bool chain = tid < NT * R;
+    const int t = tid / R, rr = tid % R;  // chain lane (token, local row)
+    float acc = 0.0f;
+    if (chain) {
         const float2* p = sP + (t * R + rr) * PB;
         const float* pm = sM + rr * PB;
         const float* pd = sDs + t * B;
-        float acc = 0.0f;
         // the chain's operands are read 16 steps at a time, so LDS latency is paid once per 16
         int b = 0;
         for (; b + 16 <= B; b += 16) {
             float2 v[16];
             float m[16], ds[16];
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
+            for (int k = 0; k < 16; k++) {
                 v[k] = p[b + k];
                 if (OFF) {
                     m[k] = pm[b + k];
@@ -1336,7 +1389,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
                 }
             }
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
+            for (int k = 0; k < 16; k++) {
                 acc = fmaf(v[k].x, v[k].y, acc);
                 if (OFF) acc = fmaf(m[k], ds[k], acc);
             }
@@ -1346,19 +1399,65 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
             acc = fmaf(v.x, v.y, acc);
             if (OFF) acc = fmaf(pm[b], pd[b], acc);
         }
-        const int orow = g * R + rr;
-        if (orow < rows) {
+    }
+
+    if (MODE == GEMM_STORE || MODE == GEMM_ADD) {
+        const int orow = global_row(rr);
+        if (chain && orow < rows) {
             float* dst = y + (int64_t)t * ldy + orow;
             *dst = MODE == GEMM_ADD ? *dst + acc : acc;
+        }
+    } else if (MODE == GEMM_QKV) {
+        // Rope.Apply on the pair (2i, 2i+1) of a head (Rope.cs:112-135): the pair's rows are
+        // neighbouring chain lanes (R and the head size are even); every chain lane takes part
+        // in the exchange, whole quads of the first wave
+        const float other = dpp_f<DPP_XOR1>(acc);
+        const int orow = global_row(rr);
+        if (chain && orow < rows) {
+            const int hh = orow / ra.hd, d = orow - hh * ra.hd, i = d >> 1;
+            const int p = ra.pos[t];
+            float v = acc;
+            if (hh < ra.n_head + ra.n_kv && i < ra.half) {
+                const float c = ra.ct[(int64_t)p * ra.half + i], s = ra.st[(int64_t)p * ra.half + i];
+                const float x0 = (d & 1) ? other : acc, x1 = (d & 1) ? acc : other;
+                v = (d & 1) ? x0 * s + x1 * c : x0 * c - x1 * s;
+            }
+            if (hh < ra.n_head) {
+                const float qs = ra.qscale[p];
+                if (qs != 1.0f) v = v * qs;  // ApplyPositionScale (MinistralModel.cs:476-482)
+                y[(int64_t)t * ldy + orow] = v;
+            } else if (hh < ra.n_head + ra.n_kv) {
+                ra.kc[((int64_t)(hh - ra.n_head) * ra.cap + ra.slot0 + t) * ra.hd + d] = v;
+            } else {
+                ra.vc[((int64_t)(hh - ra.n_head - ra.n_kv) * ra.cap + ra.slot0 + t) * ra.hd + d] = v;
+            }
+        }
+    } else {  // GEMM_SWIGLU
+        // Kernels.SwiGlu (Kernels.cs:83-90): y = sigmoid(g)·(g·u) per feature, then the block's
+        // quantization (8 lanes per token, 4 features each)
+        float* sOut = reinterpret_cast<float*>(sA);  // the codes are no longer read
+        if (chain) sOut[t * 64 + rr] = acc;
+        __syncthreads();
+        if (tid < 8 * NT) {
+            const int tq = tid >> 3, l8 = tid & 7;
+            const float* go = sOut + tq * 64 + 4 * l8;
+            const float* uo = go + 32;
+            float4 v;
+            v.x = (1.0f / (1.0f + det_expf(-go[0]))) * (go[0] * uo[0]);
+            v.y = (1.0f / (1.0f + det_expf(-go[1]))) * (go[1] * uo[1]);
+            v.z = (1.0f / (1.0f + det_expf(-go[2]))) * (go[2] * uo[2]);
+            v.w = (1.0f / (1.0f + det_expf(-go[3]))) * (go[3] * uo[3]);
+            quant_block8(v, l8, ao, tq, g, 0);
         }
     }
 }
 
 template <int TYPE, int NT, int MODE, int R>
-static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
+                                const ActQ8& ao, int n_ft, const RopeArgs& ra)
 {
     constexpr bool OFF = TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1;
-    const int n_wg = w.tiles * (32 / R);
+    const int n_wg = MODE == GEMM_SWIGLU ? n_ft : w.tiles * (32 / R);
     const size_t shm = narrow_lds_bytes(R, w.blocks, NT, OFF);
     if (shm > (64u << 10)) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_narrow<TYPE, NT, MODE, R>),
@@ -1367,55 +1466,67 @@ static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, in
     }
     dim3 grid((unsigned)((n_wg + 7) / 8 * 8)), block(256);
     hipLaunchKernelGGL((k_gemm_narrow<TYPE, NT, MODE, R>), grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.rows,
-                       w.blocks, n_wg, a, y, ldy);
+                       w.blocks, n_wg, a, y, ldy, ao, n_ft, ra);
     return hipGetLastError();
 }
 
 template <int TYPE, int NT, int MODE>
-static hipError_t narrow_rows_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+static hipError_t narrow_rows_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
+                                     const ActQ8& ao, int n_ft, const RopeArgs& ra)
 {
-    switch (narrow_rows(w)) {
-    case 32: return narrow_launch<TYPE, NT, MODE, 32>(w, a, y, ldy, s);
-    case 16: return narrow_launch<TYPE, NT, MODE, 16>(w, a, y, ldy, s);
-    default: return narrow_launch<TYPE, NT, MODE, 8>(w, a, y, ldy, s);
+    if constexpr (MODE == GEMM_SWIGLU) {
+        return narrow_launch<TYPE, NT, MODE, 64>(w, a, y, ldy, s, ao, n_ft, ra);
+    } else {
+        switch (narrow_rows(w, MODE)) {
+        case 32: return narrow_launch<TYPE, NT, MODE, 32>(w, a, y, ldy, s, ao, n_ft, ra);
+        case 16: return narrow_launch<TYPE, NT, MODE, 16>(w, a, y, ldy, s, ao, n_ft, ra);
+        default: return narrow_launch<TYPE, NT, MODE, 8>(w, a, y, ldy, s, ao, n_ft, ra);
+        }
     }
 }
 
 template <int TYPE, int MODE>
-static hipError_t narrow_mode(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s)
+static hipError_t narrow_mode(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
+                              const ActQ8& ao, int n_ft, const RopeArgs& ra)
 {
     switch (a.T) {
-    case 1: return narrow_rows_launch<TYPE, 1, MODE>(w, a, y, ldy, s);
-    case 2: return narrow_rows_launch<TYPE, 2, MODE>(w, a, y, ldy, s);
-    case 3: return narrow_rows_launch<TYPE, 3, MODE>(w, a, y, ldy, s);
-    case 4: return narrow_rows_launch<TYPE, 4, MODE>(w, a, y, ldy, s);
-    default: return hipErrorInvalidValue;
+    case 1: return narrow_rows_launch<TYPE, 1, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
+    case 2: return narrow_rows_launch<TYPE, 2, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
+    case 3: return narrow_rows_launch<TYPE, 3, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
+    default: return narrow_rows_launch<TYPE, 4, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
     }
 }
 
 template <int TYPE>
-static hipError_t narrow_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+static hipError_t narrow_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s,
+                              const ActQ8& ao, int n_ft, const RopeArgs& ra)
 {
-    return mode == GEMM_ADD ? narrow_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s) : narrow_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s);
+    switch (mode) {
+    case GEMM_ADD: return narrow_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s, ao, n_ft, ra);
+    case GEMM_SWIGLU: return narrow_mode<TYPE, GEMM_SWIGLU>(w, a, y, ldy, s, ao, n_ft, ra);
+    case GEMM_QKV: return narrow_mode<TYPE, GEMM_QKV>(w, a, y, ldy, s, ao, n_ft, ra);
+    default: return narrow_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s, ao, n_ft, ra);
+    }
 }
 
-static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
+static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s,
+                                     const ActQ8& ao, int n_ft, const RopeArgs& ra)
 {
     switch (w.type) {
-    case SHS_TYPE_Q4_0: return narrow_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s);
-    case SHS_TYPE_Q4_1: return narrow_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s);
-    case SHS_TYPE_Q5_0: return narrow_type<SHS_TYPE_Q5_0>(w, a, y, ldy, mode, s);
-    case SHS_TYPE_Q5_1: return narrow_type<SHS_TYPE_Q5_1>(w, a, y, ldy, mode, s);
-    case SHS_TYPE_Q8_0: return narrow_type<SHS_TYPE_Q8_0>(w, a, y, ldy, mode, s);
+    case SHS_TYPE_Q4_0: return narrow_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s, ao, n_ft, ra);
+    case SHS_TYPE_Q4_1: return narrow_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s, ao, n_ft, ra);
+    case SHS_TYPE_Q5_0: return narrow_type<SHS_TYPE_Q5_0>(w, a, y, ldy, mode, s, ao, n_ft, ra);
+    case SHS_TYPE_Q5_1: return narrow_type<SHS_TYPE_Q5_1>(w, a, y, ldy, mode, s, ao, n_ft, ra);
+    case SHS_TYPE_Q8_0: return narrow_type<SHS_TYPE_Q8_0>(w, a, y, ldy, mode, s, ao, n_ft, ra);
     default: return hipErrorInvalidValue;
     }
 }
 
-int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a)
+int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a, int mode)
 {
     if (a.T < 1 || a.T > NARROW_MAX_T || !type_supported(w.type)) return 0;
     const bool off = type_has_offset(w.type);
-    return narrow_lds_bytes(narrow_rows(w), w.blocks, a.T, off) <= (160u << 10) ? a.T : 0;
+    return narrow_lds_bytes(narrow_rows(w, mode), w.blocks, a.T, off) <= (160u << 10) ? a.T : 0;
 }
 
 // -------------------------------------------------------- embedding gather

@@ -157,6 +157,26 @@ def test_single_token_decode_matches_the_oracle(shs, tiny):
     assert np.array_equal(gpu.forward(toks), last)  # the same position through the wide kernels
 
 
+@pytest.mark.parametrize("qt", [3, 6, 7, 8])
+def test_decode_with_other_weight_types(shs, oracle, qt):
+    """The narrow kernels' fused q|k|v (RoPE, KV store) and gate|up (SwiGLU, quantization)
+    epilogues for the offset (Q4_1, Q5_1), fifth-bit (Q5_0, Q5_1) and Q8_0 types: a prompt,
+    then 1-, 2- and 4-token steps, bit-exact against the oracle."""
+    cfg = oracle.make_config(**TINY)
+    tensors, types = H.synth_model_tensors(oracle, cfg, qt, seed=40 + qt)
+    gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=200)
+    try:
+        toks = np.random.default_rng(qt).integers(0, cfg.vocab, 47)
+        assert np.array_equal(gpu.forward(toks[:40]), ora.forward(toks[:40], head_mode=2))
+        for a, b in ((40, 41), (41, 43), (43, 47)):
+            g = gpu.forward(toks[a:b])
+            o = ora.forward(toks[a:b], head_mode=2)
+            assert np.array_equal(g.view(np.uint32), o.view(np.uint32)), (qt, a, b, H.rel_l2(g, o))
+    finally:
+        gpu.close()
+
+
 def test_prefix_cache_is_bit_identical(shs, tiny):
     """SystemPromptCacheTests.CachedAndUncachedProduceIdenticalLogits (all vocab entries)."""
     cfg, tensors, types, gpu, ora = tiny
