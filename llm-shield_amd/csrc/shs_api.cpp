@@ -1020,7 +1020,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             if (m->max_qc <= ATT_DEC_MAX_Q && c.n_head / c.n_kv_head <= 4 &&
                 m->max_keys <= attn_decode_max_keys(m->max_qc, m->max_lds)) {
                 // decode width: scores per (KV head, 64-key chunk), values per (head, 32-dim slice)
-                Timed tk(m->prof, "k_attn_decode", attn_ops, m->stream, "attention");
+                Timed tk(m->prof, "attn_decode", attn_ops, m->stream, "attention");
                 HIP_TRY(launch_attn_decode(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head,
                                            c.head_dim, scale, m->max_qc, m->max_keys, scr, ctx, qdim,
                                            cap_on ? nullptr : &ac, m->stream));

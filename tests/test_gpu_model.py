@@ -96,7 +96,7 @@ def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
             g = gpu.forward_selected(toks, ids)
             o = ora.forward(toks, head_mode=1, vocab_ids=ids)
             assert np.array_equal(g, o), (n, H.rel_l2(g, o))
-        # decode width onto the 1100-token cache: 2 queries, then 1 (k_attn_decode)
+        # decode width onto the 1100-token cache: 2 queries, then 1 (k_attn_dec_scores + k_attn_dec_pv)
         gpu.profile(True)
         gpu.profile_reset()
         try:
@@ -104,7 +104,7 @@ def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
                 g = gpu.forward(step)
                 o = ora.forward(step, head_mode=2)
                 assert np.array_equal(g, o), H.rel_l2(g, o)
-            assert gpu.profile_read("k_attn_decode")[0] == 2 * cfg.n_layer
+            assert gpu.profile_read("attn_decode")[0] == 2 * cfg.n_layer
         finally:
             gpu.profile(False)
     finally:
@@ -113,8 +113,8 @@ def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
 
 def test_packed_batch_of_decode_width_prompts_matches_the_oracle(shs, oracle, tiny):
     """A packed batch of 1-4-token prompts: every item is decode width, so attention runs
-    k_attn_decode over 5 items and the GEMMs the narrow kernel (T = 12 > 4 takes k_gemm:
-    both widths meet in one model)."""
+    k_attn_dec_scores + k_attn_dec_pv over 5 items, while the GEMMs (T = 12 > 4) take k_gemm:
+    both widths meet in one pass."""
     cfg, tensors, types, gpu, ora = tiny
     rng = np.random.default_rng(19)
     prompts = [rng.integers(0, cfg.vocab, n) for n in (1, 4, 2, 3, 2)]
