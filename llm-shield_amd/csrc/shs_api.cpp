@@ -966,14 +966,26 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         ActQ8 ah = a;
         ah.K = hidden;
         ah.B = hidden / 32;
-        {
+        // At decode width the fused q|k|v and gate|up kernels normalize and quantize the hidden
+        // rows themselves (NormIn); otherwise k_rmsnorm_quant writes the codes first.
+        NormIn attn_in, ffn_in;
+        attn_in.x = ffn_in.x = h;
+        attn_in.ldx = ffn_in.ldx = hidden;
+        attn_in.eps = ffn_in.eps = c.rms_eps;
+        attn_in.w = L.attn_norm;
+        ffn_in.w = L.ffn_norm;
+        const bool qkv_fused = !cap_on && L.qkv.parts.size() == 1 && c.head_dim % 32 == 0;
+        const bool gu_fused = !cap_on && L.gu.parts.size() == 1;
+        const bool qkv_norm = qkv_fused && gemm_narrow_tokens(L.qkv.parts[0], ah, GEMM_QKV, true) > 0;
+        const bool gu_norm = gu_fused && gemm_narrow_tokens(L.gu.parts[0], ah, GEMM_SWIGLU, true) > 0;
+        if (!qkv_norm) {
             Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
             HIP_TRY(launch_rmsnorm_quant(h, hidden, L.attn_norm, c.rms_eps, hidden, ah, normed, m->stream));
         }
         snprintf(name, sizeof name, "blk.%d.attn_norm", l);
         if (cap_on && cp.observe(name, normed, hidden, T, hidden) != SHS_OK) return SHS_E_DEVICE;
 
-        if (!cap_on && L.qkv.parts.size() == 1 && c.head_dim % 32 == 0) {
+        if (qkv_fused) {
             // one fused matrix: RoPE and the KV-cache store in the epilogue
             RopeArgs ra;
             ra.pos = m->pos.as<int32_t>();
@@ -992,7 +1004,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             char kname[48] = "k_gemm";
             if (m->prof.on) gemm_kname(kname, sizeof kname, w, ah, GEMM_QKV);
             Timed tm(m->prof, "gemm_qkv", gemm_ops(T, w), m->stream, kname);
-            HIP_TRY(launch_gemm_qkv(w, ah, qkv, ldqkv, ra, m->stream));
+            HIP_TRY(launch_gemm_qkv(w, ah, qkv, ldqkv, ra, m->stream, qkv_norm ? &attn_in : nullptr));
         } else {
             if (run_proj(m, L.qkv, ah, qkv, ldqkv, GEMM_STORE, "gemm_qkv") != SHS_OK) return SHS_E_DEVICE;
             Timed tm(m->prof, "rope_store", 0, m->stream);
@@ -1068,7 +1080,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             if (run_proj(m, L.o, ac, h, hidden, GEMM_ADD, "gemm_o") != SHS_OK) return SHS_E_DEVICE;
         }
 
-        {
+        if (!gu_norm) {
             Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
             HIP_TRY(launch_rmsnorm_quant(h, hidden, L.ffn_norm, c.rms_eps, hidden, ah, normed, m->stream));
         }
@@ -1078,14 +1090,14 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         ActQ8 af = a;
         af.K = c.ffn;
         af.B = c.ffn / 32;
-        if (!cap_on && L.gu.parts.size() == 1) {
+        if (gu_fused) {
             // one fused matrix: SwiGLU and the down projection's quantization in the epilogue
             HIP_TRY(m->act_ffn.ensure(T, c.ffn, &af));
             const DevMatrix& w = L.gu.parts[0];
             char kname[48] = "k_gemm";
             if (m->prof.on) gemm_kname(kname, sizeof kname, w, ah, GEMM_SWIGLU);
             Timed tm(m->prof, "gemm_gate_up", gemm_ops(T, w), m->stream, kname);
-            HIP_TRY(launch_gemm_swiglu(w, ah, c.ffn / 32, af, m->stream));
+            HIP_TRY(launch_gemm_swiglu(w, ah, c.ffn / 32, af, m->stream, gu_norm ? &ffn_in : nullptr));
         } else {
             if (run_proj(m, L.gu, ah, gu, 2 * c.ffn, GEMM_STORE, "gemm_gate_up") != SHS_OK) return SHS_E_DEVICE;
             Timed tm(m->prof, "swiglu_quant", 0, m->stream);

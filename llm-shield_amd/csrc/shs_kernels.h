@@ -80,6 +80,17 @@ struct RopeArgs {
     int cap = 0, slot0 = 0;
 };
 
+// The input of a narrow q|k|v or gate|up GEMM given as the hidden rows instead of codes:
+// every work-group applies Kernels.RmsNorm with gain w to rows x (T of them, stride ldx)
+// and quantizes the result itself, while its weight loads are in flight — the same
+// arithmetic as k_rmsnorm_quant, so the codes are the same bits.
+struct NormIn {
+    const float* x = nullptr;
+    int ldx = 0;
+    const float* w = nullptr;
+    float eps = 0.0f;
+};
+
 int qs_bytes(int type);
 bool type_supported(int type);
 bool type_has_offset(int type);
@@ -93,16 +104,20 @@ hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float e
 hipError_t launch_swiglu_quant(const float* gu, int ldgu, int ffn, const ActQ8& a, float* y_opt, hipStream_t s);
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s);
 // y = SwiGLU(x·[gate|up]ᵀ) quantized into `out` (K = 32·n_ft); w holds 2·n_ft row tiles.
-hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s);
+hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s,
+                              const NormIn* norm = nullptr);
 // q|k|v = x·Wᵀ with RoPE: rotated (and scaled) q into y, rotated k and v into the cache.
-hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s);
+hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s,
+                           const NormIn* norm = nullptr);
 // The token tiles per block launch_gemm picks for this shape (the k_gemm instantiation's TT).
 int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode);
 // Up to NARROW_MAX_T tokens, launch_gemm, launch_gemm_qkv and launch_gemm_swiglu stream the
 // weights through k_gemm_narrow instead (same epilogues); returns the token count when they
-// do for this mode, else 0.
+// do for this mode, else 0. With `with_norm`, whether the kernel can also form its input
+// itself (NormIn).
 enum { NARROW_MAX_T = 4 };
-int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a, int mode);
+int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a, int mode, bool with_norm = false);
+
 hipError_t launch_gemm_block_sums(const DevMatrix& w, const ActQ8& a, int32_t* out, hipStream_t s);
 hipError_t launch_gemv_rows(const DevMatrix& w, const ActQ8& a, const int32_t* row_ids, int n_ids, float* y,
                             hipStream_t s);

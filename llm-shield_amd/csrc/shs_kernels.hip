@@ -195,7 +195,15 @@ __device__ __forceinline__ float vsum8_lanes(float v)
 // float(Σq) and d·Σq, the offset types' second epilogue factor. The 8 lanes of an aligned
 // lane group (l8 = lane % 8) hold elements 4·l8 .. 4·l8+3; max and Σq are exact in any
 // order, so the group reductions are order-free. Each lane stores its 4 int8 codes.
-__device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, int t, int b, int semantics)
+// The quantization of one block, without its stores: the lane's 4 codes packed in a word,
+// the block's d (as stored) and Σq (both the same in every lane of the group).
+struct QBlock {
+    uint32_t w;
+    float d;
+    int sum;
+};
+
+__device__ __forceinline__ QBlock quant_block8_values(float4 v, int semantics)
 {
     float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
     mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
@@ -224,11 +232,17 @@ __device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, i
     sum += dpp_i<DPP_HALF_MIRROR>(sum);
     const uint32_t w = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
                        ((uint32_t)(q3 & 0xFF) << 24);
-    *reinterpret_cast<uint32_t*>(a.q + act_code_offset(a, t, b, l8)) = w;
+    return QBlock{w, dd, sum};
+}
+
+__device__ __forceinline__ void quant_block8(float4 v, int l8, const ActQ8& a, int t, int b, int semantics)
+{
+    const QBlock qb = quant_block8_values(v, semantics);
+    *reinterpret_cast<uint32_t*>(a.q + act_code_offset(a, t, b, l8)) = qb.w;
     if (l8 == 0) {
-        a.d[(int64_t)b * a.Tpad + t] = dd;
-        a.cv[(int64_t)b * a.Tpad + t] = conversion_operand(sum);
-        a.ds[(int64_t)b * a.Tpad + t] = dd * (float)sum;
+        a.d[(int64_t)b * a.Tpad + t] = qb.d;
+        a.cv[(int64_t)b * a.Tpad + t] = conversion_operand(qb.sum);
+        a.ds[(int64_t)b * a.Tpad + t] = qb.d * (float)qb.sum;
     }
 }
 
@@ -278,14 +292,13 @@ __device__ inline float vsum8(const float* a)
 
 // Kernels.RmsNorm (Kernels.cs:26-61) in its own order — 16 running float sums of x²
 // (8 "even" lanes, 8 "odd" lanes of Vector<float>), each pairwise-summed and widened to
-// double — followed by y = (x·s)·w and the 32-block quantization of y: token t's row xr,
+// double — followed by y = (x·s)·w, handed 4 elements at a time to `sink(v, l8, b)` (the
+// lanes l8 = 0..7 of an aligned group hold block b's elements 4·l8 .. 4·l8+3): token row xr,
 // by a whole block of 256 threads. LDS: sx holds 2n floats (the row, then its squares),
-// part 16 floats and s_scale one. Ends with the block's threads past a barrier only if the
-// caller adds one (the next use of sx must be preceded by __syncthreads()).
-__device__ __forceinline__ void rmsnorm_quant_token(const float* __restrict__ xr, const float* __restrict__ w,
-                                                    float eps, int n, const ActQ8& a, int t,
-                                                    float* __restrict__ y_row, float* sx, float* part,
-                                                    float* s_scale)
+// part 16 floats and s_scale one. The next use of sx must be preceded by __syncthreads().
+template <class Sink>
+__device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const float* __restrict__ w, float eps,
+                                             int n, float* sx, float* part, float* s_scale, Sink&& sink)
 {
     const int tid = threadIdx.x;
     float* sq = sx + n;
@@ -297,7 +310,7 @@ __device__ __forceinline__ void rmsnorm_quant_token(const float* __restrict__ xr
 #pragma unroll
     for (int i = 0; i < WPRE; i++) {
         const int b = (tid >> 3) + (256 >> 3) * i;
-        wpre[i] = b < a.B ? *reinterpret_cast<const float4*>(w + 32 * b + 4 * l8) : make_float4(0.f, 0.f, 0.f, 0.f);
+        wpre[i] = b < n / 32 ? *reinterpret_cast<const float4*>(w + 32 * b + 4 * l8) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (n & 3) == 0) {
         // float4 row copy, the loads of a thread issued together; the squares x·x (rounded,
@@ -346,7 +359,7 @@ __device__ __forceinline__ void rmsnorm_quant_token(const float* __restrict__ xr
     __syncthreads();
     const float sc = *s_scale;
     int i = 0;
-    for (int b = tid >> 3; b < a.B; b += 256 >> 3, i++) {  // uniform per 8-lane group
+    for (int b = tid >> 3; b < n / 32; b += 256 >> 3, i++) {  // uniform per 8-lane group
         const int e = 32 * b + 4 * l8;
         const float4 xv = *reinterpret_cast<const float4*>(sx + e);
         float4 wv;
@@ -361,8 +374,7 @@ __device__ __forceinline__ void rmsnorm_quant_token(const float* __restrict__ xr
         v.y = (xv.y * sc) * wv.y;
         v.z = (xv.z * sc) * wv.z;
         v.w = (xv.w * sc) * wv.w;
-        if (y_row) *reinterpret_cast<float4*>(y_row + e) = v;
-        quant_block8(v, l8, a, t, b, 0);
+        sink(v, l8, b);
     }
 }
 
@@ -379,8 +391,11 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
         for (int b = tid >> 3; b < a.B; b += blockDim.x >> 3) zero_block8(tid & 7, a, t, b);
         return;
     }
-    rmsnorm_quant_token(x + (int64_t)t * ldx, w, eps, n, a, t, y_opt ? y_opt + (int64_t)t * n : nullptr, sx, part,
-                        &s_scale);
+    float* y_row = y_opt ? y_opt + (int64_t)t * n : nullptr;
+    rmsnorm_rows(x + (int64_t)t * ldx, w, eps, n, sx, part, &s_scale, [&](float4 v, int l8, int b) {
+        if (y_row) *reinterpret_cast<float4*>(y_row + 32 * b + 4 * l8) = v;
+        quant_block8(v, l8, a, t, b, 0);
+    });
 }
 
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float eps, int n, const ActQ8& a,
@@ -931,7 +946,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
 }
 
 static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s,
-                                     const ActQ8& ao, int n_ft, const RopeArgs& ra);
+                                     const ActQ8& ao, int n_ft, const RopeArgs& ra, const NormIn& nin);
 
 template <int TYPE, int TT, int MODE>
 static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
@@ -1029,11 +1044,16 @@ int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode)
     }
 }
 
-hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s)
+hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, const ActQ8& out, hipStream_t s,
+                              const NormIn* norm)
 {
     if (w.tiles != 2 * n_ft || out.B != n_ft || out.Tpad != a.Tpad) return hipErrorInvalidValue;
+    if (norm) {
+        if (gemm_narrow_tokens(w, a, GEMM_SWIGLU, true) == 0) return hipErrorInvalidValue;
+        return launch_gemm_narrow(w, a, nullptr, 0, GEMM_SWIGLU, s, out, n_ft, RopeArgs(), *norm);
+    }
     if (gemm_narrow_tokens(w, a, GEMM_SWIGLU) > 0)
-        return launch_gemm_narrow(w, a, nullptr, 0, GEMM_SWIGLU, s, out, n_ft, RopeArgs());
+        return launch_gemm_narrow(w, a, nullptr, 0, GEMM_SWIGLU, s, out, n_ft, RopeArgs(), NormIn());
     switch (w.type) {
     case SHS_TYPE_Q4_0: return gemm_swiglu_type<SHS_TYPE_Q4_0>(w, a, n_ft, out, s);
     case SHS_TYPE_Q4_1: return gemm_swiglu_type<SHS_TYPE_Q4_1>(w, a, n_ft, out, s);
@@ -1044,13 +1064,18 @@ hipError_t launch_gemm_swiglu(const DevMatrix& w, const ActQ8& a, int n_ft, cons
     }
 }
 
-hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s)
+hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy, const RopeArgs& ra, hipStream_t s,
+                           const NormIn* norm)
 {
     if (ra.hd % 32 != 0 || w.rows != (ra.n_head + 2 * ra.n_kv) * ra.hd || (ldy & 3) != 0 ||
         (reinterpret_cast<uintptr_t>(y) & 15) != 0)
         return hipErrorInvalidValue;
+    if (norm) {
+        if (gemm_narrow_tokens(w, a, GEMM_QKV, true) == 0) return hipErrorInvalidValue;
+        return launch_gemm_narrow(w, a, y, ldy, GEMM_QKV, s, ActQ8(), 0, ra, *norm);
+    }
     if (gemm_narrow_tokens(w, a, GEMM_QKV) > 0)
-        return launch_gemm_narrow(w, a, y, ldy, GEMM_QKV, s, ActQ8(), 0, ra);
+        return launch_gemm_narrow(w, a, y, ldy, GEMM_QKV, s, ActQ8(), 0, ra, NormIn());
     switch (w.type) {
     case SHS_TYPE_Q4_0: return gemm_qkv_type<SHS_TYPE_Q4_0>(w, a, y, ldy, ra, s);
     case SHS_TYPE_Q4_1: return gemm_qkv_type<SHS_TYPE_Q4_1>(w, a, y, ldy, ra, s);
@@ -1064,7 +1089,7 @@ hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy
 hipError_t launch_gemm(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s)
 {
     if ((mode == GEMM_STORE || mode == GEMM_ADD) && gemm_narrow_tokens(w, a, mode) > 0)
-        return launch_gemm_narrow(w, a, y, ldy, mode, s, ActQ8(), 0, RopeArgs());
+        return launch_gemm_narrow(w, a, y, ldy, mode, s, ActQ8(), 0, RopeArgs(), NormIn());
     switch (w.type) {
     case SHS_TYPE_Q4_0: return gemm_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s);
     case SHS_TYPE_Q4_1: return gemm_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s);
@@ -1281,7 +1306,7 @@ template <int TYPE, int NT, int MODE, int R>
 __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                      const float* __restrict__ wd, const float* __restrict__ wm,
                                                      int rows, int B, int n_wg, ActQ8 a, float* __restrict__ y, int ldy,
-                                                     ActQ8 ao, int n_ft, RopeArgs ra)
+                                                     ActQ8 ao, int n_ft, RopeArgs ra, NormIn nin)
 {
     constexpr bool OFF = TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1;
     constexpr bool Q8 = TYPE == SHS_TYPE_Q8_0;
@@ -1313,24 +1338,47 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     NarrowBatch<TYPE, NB> cur, nxt;
     narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
 
-    for (int i = tid; i < NT * B * 2; i += 256) {
-        const int t = i / (2 * B), rem = i - t * 2 * B, b = rem >> 1, h = rem & 1;
-        sA[i] = *reinterpret_cast<const uint4*>(a.q + (((int64_t)(t >> 5) * B + b) * 64 + (t & 31)) * 16 + h * 512);
-    }
-    for (int i = tid; i < NT * B; i += 256) {
-        const int t = i / B, b = i - t * B;
-        const int64_t k = (int64_t)b * a.Tpad + t;
-        sDa[i] = a.d[k];
-        if (OFF) sDs[i] = a.ds[k];
-        if (Z != 0) {
-            // the conversion column holds fp16 (−6144, −hi, −lo, 0) with Σa = 64·hi + lo
-            const uint2 cv = a.cv[k];
-            const int hi = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(cv.x >> 16));
-            const int lo = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(cv.y & 0xFFFFu));
-            sSum[i] = -(64 * hi + lo);
+    if (nin.x) {
+        // the codes formed here from the hidden rows: Kernels.RmsNorm, then the 32-block
+        // quantization, into the arrays the staged codes would fill (the row's scratch follows)
+        float* nsx = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(sDs + NT * B) + 15) & ~(uintptr_t)15);
+        uint8_t* sAb = reinterpret_cast<uint8_t*>(sA);
+        const int K = 32 * B;
+        for (int t = 0; t < NT; ++t) {
+            rmsnorm_rows(nin.x + (int64_t)t * nin.ldx, nin.w, nin.eps, K, nsx, nsx + 2 * K, nsx + 2 * K + 16,
+                         [&](float4 v, int l8, int b) {
+                             const QBlock qb = quant_block8_values(v, 0);
+                             // element group 4·l8 .. +3 sits in half (l8 >> 1) & 1 (the act_code_offset order)
+                             const int hf = (l8 >> 1) & 1, idx = 4 * (l8 & 1) + 8 * (l8 >> 2);
+                             *reinterpret_cast<uint32_t*>(sAb + ((t * B + b) * 2 + hf) * 16 + idx) = qb.w;
+                             if (l8 == 0) {
+                                 sDa[t * B + b] = qb.d;
+                                 sSum[t * B + b] = qb.sum;
+                                 sDs[t * B + b] = qb.d * (float)qb.sum;
+                             }
+                         });
+            __syncthreads();
         }
+    } else {
+        for (int i = tid; i < NT * B * 2; i += 256) {
+            const int t = i / (2 * B), rem = i - t * 2 * B, b = rem >> 1, h = rem & 1;
+            sA[i] = *reinterpret_cast<const uint4*>(a.q + (((int64_t)(t >> 5) * B + b) * 64 + (t & 31)) * 16 + h * 512);
+        }
+        for (int i = tid; i < NT * B; i += 256) {
+            const int t = i / B, b = i - t * B;
+            const int64_t k = (int64_t)b * a.Tpad + t;
+            sDa[i] = a.d[k];
+            if (OFF) sDs[i] = a.ds[k];
+            if (Z != 0) {
+                // the conversion column holds fp16 (−6144, −hi, −lo, 0) with Σa = 64·hi + lo
+                const uint2 cv = a.cv[k];
+                const int hi = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(cv.x >> 16));
+                const int lo = (int)(float)__builtin_bit_cast(_Float16, (uint16_t)(cv.y & 0xFFFFu));
+                sSum[i] = -(64 * hi + lo);
+            }
+        }
+        __syncthreads();
     }
-    __syncthreads();
 
     // batches of NB·BS blocks; the next batch is prefetched only when there is one (a barrier
     // waits for every load in flight)
@@ -1452,13 +1500,17 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     }
 }
 
+// LDS for a work-group that forms its own codes (NormIn): one hidden row and its squares,
+// then the 16 running sums and the scale
+static size_t narrow_norm_lds_bytes(int B) { return sizeof(float) * (2 * 32 * (size_t)B + 17) + 16; }
+
 template <int TYPE, int NT, int MODE, int R>
 static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
-                                const ActQ8& ao, int n_ft, const RopeArgs& ra)
+                                const ActQ8& ao, int n_ft, const RopeArgs& ra, const NormIn& nin)
 {
     constexpr bool OFF = TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1;
     const int n_wg = MODE == GEMM_SWIGLU ? n_ft : w.tiles * (32 / R);
-    const size_t shm = narrow_lds_bytes(R, w.blocks, NT, OFF);
+    const size_t shm = narrow_lds_bytes(R, w.blocks, NT, OFF) + (nin.x ? narrow_norm_lds_bytes(w.blocks) : 0);
     if (shm > (64u << 10)) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_narrow<TYPE, NT, MODE, R>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
@@ -1466,67 +1518,69 @@ static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, in
     }
     dim3 grid((unsigned)((n_wg + 7) / 8 * 8)), block(256);
     hipLaunchKernelGGL((k_gemm_narrow<TYPE, NT, MODE, R>), grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.rows,
-                       w.blocks, n_wg, a, y, ldy, ao, n_ft, ra);
+                       w.blocks, n_wg, a, y, ldy, ao, n_ft, ra, nin);
     return hipGetLastError();
 }
 
 template <int TYPE, int NT, int MODE>
 static hipError_t narrow_rows_launch(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
-                                     const ActQ8& ao, int n_ft, const RopeArgs& ra)
+                                     const ActQ8& ao, int n_ft, const RopeArgs& ra, const NormIn& nin)
 {
     if constexpr (MODE == GEMM_SWIGLU) {
-        return narrow_launch<TYPE, NT, MODE, 64>(w, a, y, ldy, s, ao, n_ft, ra);
+        return narrow_launch<TYPE, NT, MODE, 64>(w, a, y, ldy, s, ao, n_ft, ra, nin);
     } else {
         switch (narrow_rows(w, MODE)) {
-        case 32: return narrow_launch<TYPE, NT, MODE, 32>(w, a, y, ldy, s, ao, n_ft, ra);
-        case 16: return narrow_launch<TYPE, NT, MODE, 16>(w, a, y, ldy, s, ao, n_ft, ra);
-        default: return narrow_launch<TYPE, NT, MODE, 8>(w, a, y, ldy, s, ao, n_ft, ra);
+        case 32: return narrow_launch<TYPE, NT, MODE, 32>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+        case 16: return narrow_launch<TYPE, NT, MODE, 16>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+        default: return narrow_launch<TYPE, NT, MODE, 8>(w, a, y, ldy, s, ao, n_ft, ra, nin);
         }
     }
 }
 
 template <int TYPE, int MODE>
 static hipError_t narrow_mode(const DevMatrix& w, const ActQ8& a, float* y, int ldy, hipStream_t s,
-                              const ActQ8& ao, int n_ft, const RopeArgs& ra)
+                              const ActQ8& ao, int n_ft, const RopeArgs& ra, const NormIn& nin)
 {
     switch (a.T) {
-    case 1: return narrow_rows_launch<TYPE, 1, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
-    case 2: return narrow_rows_launch<TYPE, 2, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
-    case 3: return narrow_rows_launch<TYPE, 3, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
-    default: return narrow_rows_launch<TYPE, 4, MODE>(w, a, y, ldy, s, ao, n_ft, ra);
+    case 1: return narrow_rows_launch<TYPE, 1, MODE>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+    case 2: return narrow_rows_launch<TYPE, 2, MODE>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+    case 3: return narrow_rows_launch<TYPE, 3, MODE>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+    default: return narrow_rows_launch<TYPE, 4, MODE>(w, a, y, ldy, s, ao, n_ft, ra, nin);
     }
 }
 
 template <int TYPE>
 static hipError_t narrow_type(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s,
-                              const ActQ8& ao, int n_ft, const RopeArgs& ra)
+                              const ActQ8& ao, int n_ft, const RopeArgs& ra, const NormIn& nin)
 {
     switch (mode) {
-    case GEMM_ADD: return narrow_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s, ao, n_ft, ra);
-    case GEMM_SWIGLU: return narrow_mode<TYPE, GEMM_SWIGLU>(w, a, y, ldy, s, ao, n_ft, ra);
-    case GEMM_QKV: return narrow_mode<TYPE, GEMM_QKV>(w, a, y, ldy, s, ao, n_ft, ra);
-    default: return narrow_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s, ao, n_ft, ra);
+    case GEMM_ADD: return narrow_mode<TYPE, GEMM_ADD>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+    case GEMM_SWIGLU: return narrow_mode<TYPE, GEMM_SWIGLU>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+    case GEMM_QKV: return narrow_mode<TYPE, GEMM_QKV>(w, a, y, ldy, s, ao, n_ft, ra, nin);
+    default: return narrow_mode<TYPE, GEMM_STORE>(w, a, y, ldy, s, ao, n_ft, ra, nin);
     }
 }
 
 static hipError_t launch_gemm_narrow(const DevMatrix& w, const ActQ8& a, float* y, int ldy, int mode, hipStream_t s,
-                                     const ActQ8& ao, int n_ft, const RopeArgs& ra)
+                                     const ActQ8& ao, int n_ft, const RopeArgs& ra, const NormIn& nin)
 {
     switch (w.type) {
-    case SHS_TYPE_Q4_0: return narrow_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s, ao, n_ft, ra);
-    case SHS_TYPE_Q4_1: return narrow_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s, ao, n_ft, ra);
-    case SHS_TYPE_Q5_0: return narrow_type<SHS_TYPE_Q5_0>(w, a, y, ldy, mode, s, ao, n_ft, ra);
-    case SHS_TYPE_Q5_1: return narrow_type<SHS_TYPE_Q5_1>(w, a, y, ldy, mode, s, ao, n_ft, ra);
-    case SHS_TYPE_Q8_0: return narrow_type<SHS_TYPE_Q8_0>(w, a, y, ldy, mode, s, ao, n_ft, ra);
+    case SHS_TYPE_Q4_0: return narrow_type<SHS_TYPE_Q4_0>(w, a, y, ldy, mode, s, ao, n_ft, ra, nin);
+    case SHS_TYPE_Q4_1: return narrow_type<SHS_TYPE_Q4_1>(w, a, y, ldy, mode, s, ao, n_ft, ra, nin);
+    case SHS_TYPE_Q5_0: return narrow_type<SHS_TYPE_Q5_0>(w, a, y, ldy, mode, s, ao, n_ft, ra, nin);
+    case SHS_TYPE_Q5_1: return narrow_type<SHS_TYPE_Q5_1>(w, a, y, ldy, mode, s, ao, n_ft, ra, nin);
+    case SHS_TYPE_Q8_0: return narrow_type<SHS_TYPE_Q8_0>(w, a, y, ldy, mode, s, ao, n_ft, ra, nin);
     default: return hipErrorInvalidValue;
     }
 }
 
-int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a, int mode)
+int gemm_narrow_tokens(const DevMatrix& w, const ActQ8& a, int mode, bool with_norm)
 {
     if (a.T < 1 || a.T > NARROW_MAX_T || !type_supported(w.type)) return 0;
     const bool off = type_has_offset(w.type);
-    return narrow_lds_bytes(narrow_rows(w, mode), w.blocks, a.T, off) <= (160u << 10) ? a.T : 0;
+    const size_t lds = narrow_lds_bytes(narrow_rows(w, mode), w.blocks, a.T, off) +
+                       (with_norm ? narrow_norm_lds_bytes(w.blocks) : 0);
+    return lds <= (160u << 10) ? a.T : 0;
 }
 
 // -------------------------------------------------------- embedding gather
