@@ -43,12 +43,9 @@ struct ActQ8 {
     float* ds = nullptr;
 };
 
-// Work item of the attention kernel: queries [q_start, q_start+q_count) of one
-// sequence, whose first query sits at position pos0 and whose keys live at cache
-// index key_start + p for p in [0, pos0 + q_count). Scores of the item's heads go to
-// scratch + s_off.
-// One attention work item: q_count ≤ 32 queries at rows q_start.. of q/ctx, attending to
-// keys key_start .. key_start + pos0 + q_count − 1 of the cache (query i sees pos0 + i + 1).
+// One attention work item: q_count ≤ 32 queries of one sequence at rows q_start.. of q/ctx,
+// the first at position pos0, attending to cache indices key_start .. key_start + pos0 +
+// q_count − 1 (query i sees pos0 + i + 1 keys). Scores of the item's heads go to scratch + s_off.
 struct AttnItem {
     int q_start, q_count, key_start, pos0;
     int64_t s_off;  // float offset of the item's score tiles: n_kv · 4 · n_tiles tiles of 1024 floats
