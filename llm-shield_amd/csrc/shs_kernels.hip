@@ -1425,25 +1425,44 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
         const float2* p = sP + (t * R + rr) * PB;
         const float* pm = sM + rr * PB;
         const float* pd = sDs + t * B;
-        // the chain's operands are read 16 steps at a time, so LDS latency is paid once per 16
+        // The chain's operands are read 16 steps at a time into two alternating register sets:
+        // the next 16 steps' reads are issued (kept ahead by an empty asm that takes acc) before the
+        // current 16 FMAs run, so the LDS latency is paid about once instead of once per 16
+        // steps.
+        const int bfull = B & ~15;
+        float2 va[16], vb[16];
+        float ma[16], da[16], mb[16], db[16];
+#define SHS_CHAIN_LOAD(V, M, D, B0)                            \
+    _Pragma("unroll") for (int k = 0; k < 16; k++)             \
+    {                                                          \
+        V[k] = p[(B0) + k];                                    \
+        if (OFF) {                                             \
+            M[k] = pm[(B0) + k];                               \
+            D[k] = pd[(B0) + k];                               \
+        }                                                      \
+    }                                                          \
+    asm volatile("" : "+v"(acc)::"memory");
+#define SHS_CHAIN_RUN(V, M, D)                                 \
+    _Pragma("unroll") for (int k = 0; k < 16; k++)             \
+    {                                                          \
+        acc = fmaf(V[k].x, V[k].y, acc);                       \
+        if (OFF) acc = fmaf(M[k], D[k], acc);                  \
+    }
         int b = 0;
-        for (; b + 16 <= B; b += 16) {
-            float2 v[16];
-            float m[16], ds[16];
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                v[k] = p[b + k];
-                if (OFF) {
-                    m[k] = pm[b + k];
-                    ds[k] = pd[b + k];
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                acc = fmaf(v[k].x, v[k].y, acc);
-                if (OFF) acc = fmaf(m[k], ds[k], acc);
-            }
+        if (bfull > 0) SHS_CHAIN_LOAD(va, ma, da, 0);
+        for (; b + 32 <= bfull; b += 32) {
+            SHS_CHAIN_LOAD(vb, mb, db, b + 16);
+            SHS_CHAIN_RUN(va, ma, da);
+            // (no round after the next: the current one again, unused, from a uniform base)
+            SHS_CHAIN_LOAD(va, ma, da, b + 48 <= bfull ? b + 32 : b);
+            SHS_CHAIN_RUN(vb, mb, db);
         }
+        if (b < bfull) {
+            SHS_CHAIN_RUN(va, ma, da);
+            b += 16;
+        }
+#undef SHS_CHAIN_LOAD
+#undef SHS_CHAIN_RUN
         for (; b < B; ++b) {
             const float2 v = p[b];
             acc = fmaf(v.x, v.y, acc);
