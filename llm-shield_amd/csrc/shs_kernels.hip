@@ -2742,9 +2742,42 @@ __global__ __launch_bounds__(256) void k_attn_dec_pv(const float* __restrict__ v
                     acc = fmaf(v[4 * g + 3], w4[g].w, acc);
                 }
             };
+            // Full groups alternate between two register sets: the next group's reads are
+            // issued (kept ahead by an empty asm that takes acc) before the current group's
+            // FMAs, so the LDS latency is paid about once per chunk.
             const int kfull = k0 + ((k1 - k0) & ~15);
             int key = k0;
-            for (; key < kfull; key += 16) group(key, false);
+            float va[16], vb[16];
+            float4 wa[4], wb[4];
+#define SHS_DEC_LOAD(V, W, KEY)                                                        \
+    {                                                                                  \
+        _Pragma("unroll") for (int g = 0; g < 4; g++) W[g] =                           \
+            *reinterpret_cast<const float4*>(w + (KEY) + 4 * g);                      \
+        _Pragma("unroll") for (int k = 0; k < 16; k++) V[k] = sV[((KEY) - k0 + k) * 32 + d]; \
+        asm volatile("" : "+v"(acc)::"memory");                                        \
+    }
+#define SHS_DEC_RUN(V, W)                                                              \
+    _Pragma("unroll") for (int g = 0; g < 4; g++)                                      \
+    {                                                                                  \
+        acc = fmaf(V[4 * g], W[g].x, acc);                                             \
+        acc = fmaf(V[4 * g + 1], W[g].y, acc);                                         \
+        acc = fmaf(V[4 * g + 2], W[g].z, acc);                                         \
+        acc = fmaf(V[4 * g + 3], W[g].w, acc);                                         \
+    }
+            if (key < kfull) SHS_DEC_LOAD(va, wa, key);
+            for (; key + 32 <= kfull; key += 32) {
+                SHS_DEC_LOAD(vb, wb, key + 16);
+                SHS_DEC_RUN(va, wa);
+                // (no group after the next: the current one again, unused)
+                SHS_DEC_LOAD(va, wa, key + 48 <= kfull ? key + 32 : key);
+                SHS_DEC_RUN(vb, wb);
+            }
+            if (key < kfull) {
+                SHS_DEC_RUN(va, wa);
+                key += 16;
+            }
+#undef SHS_DEC_LOAD
+#undef SHS_DEC_RUN
             if (key < k1) group(key, true);
         }
     }
