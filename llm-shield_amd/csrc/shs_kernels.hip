@@ -331,17 +331,38 @@ __device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const
     __syncthreads();
     if (tid < 16) {
         // lane tid's running sum over elements tid + 16k in order; the reads of 16 steps are
-        // issued together, the adds stay one chain
+        // issued together into one of two register sets, the next 16 (kept ahead by an empty
+        // asm that takes acc) before the current 16 adds, which stay one chain
         float acc = 0.0f;
         const int nk = n / 16;
+        const int kfull = nk & ~15;
         int k = 0;
-        for (; k + 16 <= nk; k += 16) {
-            float v[16];
-#pragma unroll
-            for (int q = 0; q < 16; q++) v[q] = sq[(k + q) * 16 + tid];
-#pragma unroll
-            for (int q = 0; q < 16; q++) acc = acc + v[q];
+        float va[16], vb[16];
+#define SHS_SQ_LOAD(V, K0)                                                        \
+    {                                                                             \
+        _Pragma("unroll") for (int q = 0; q < 16; q++) V[q] = sq[((K0) + q) * 16 + tid]; \
+        asm volatile("" : "+v"(acc)::"memory");                                   \
+    }
+#define SHS_SQ_RUN(V)                                                             \
+    {                                                                             \
+        _Pragma("unroll") for (int q = 0; q < 16; q++) acc = acc + V[q];          \
+        asm volatile("" : "+v"(acc)::"memory");                                   \
+    }
+        if (kfull > 0) {
+            SHS_SQ_LOAD(va, 0);
+            for (; k + 32 <= kfull; k += 32) {
+                SHS_SQ_LOAD(vb, k + 16);
+                SHS_SQ_RUN(va);
+                SHS_SQ_LOAD(va, k + 48 <= kfull ? k + 32 : k);  // past the last group: unused
+                SHS_SQ_RUN(vb);
+            }
+            if (k < kfull) {
+                SHS_SQ_RUN(va);
+                k += 16;
+            }
         }
+#undef SHS_SQ_LOAD
+#undef SHS_SQ_RUN
         for (; k < nk; k++) acc = acc + sq[k * 16 + tid];
         part[tid] = acc;
     }
