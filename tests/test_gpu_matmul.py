@@ -88,9 +88,12 @@ def test_decode_widths_are_bit_exact(lib, oracle, qt):
     """1-4 tokens take the weight-streaming narrow kernel: bit-exact against the oracle and
     against the same tokens inside a wide batch, with a partial row tile, an odd block
     count (7), the down projection's 288 blocks and the row counts that take 16-row (from
-    16384 rows) and 32-row (from 65536, the vocabulary head) work-groups."""
+    16384 rows) and 32-row (from 65536, the vocabulary head) work-groups. The serial chain
+    reads its operands in rounds of 16 blocks, alternating two register sets: 96 and 288
+    blocks are an even number of rounds, 48 an odd one, 81 an odd one plus a remainder, 7 no
+    full round."""
     rng = np.random.default_rng(20 + qt)
-    for rows, cols in [(100, 3072), (64, 224), (40, 9216), (20001, 256), (65601, 256)]:
+    for rows, cols in [(100, 3072), (64, 224), (40, 9216), (20001, 256), (65601, 256), (50, 1536), (24, 2592)]:
         w = H.random_blocks(qt, rows, cols, seed=rows + cols + qt)
         m = lib.WeightMatrix(qt, rows, cols, w)
         x = (rng.random((40, cols)) * 2 - 1).astype(np.float32)
