@@ -290,15 +290,27 @@ __device__ inline float vsum8(const float* a)
     return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
 }
 
+// A work-group barrier that waits only for this wave's LDS operations. Global loads in flight
+// (a caller's prefetched weights) stay in flight, where __syncthreads() (s_waitcnt vmcnt(0))
+// would wait for them; only LDS data may be handed between waves across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Kernels.RmsNorm (Kernels.cs:26-61) in its own order — 16 running float sums of x²
 // (8 "even" lanes, 8 "odd" lanes of Vector<float>), each pairwise-summed and widened to
 // double — followed by y = (x·s)·w, handed 4 elements at a time to `sink(v, l8, b)` (the
 // lanes l8 = 0..7 of an aligned group hold block b's elements 4·l8 .. 4·l8+3): token row xr,
 // by a whole block of 256 threads. LDS: sx holds 2n floats (the row, then its squares),
-// part 16 floats and s_scale one. The next use of sx must be preceded by __syncthreads().
-template <class Sink>
+// part 16 floats and s_scale one. The next use of sx must be preceded by a barrier.
+// `issue()` runs right after the row's loads are issued and before they are used: loads it
+// issues stay in flight through the normalization (global loads complete in issue order, and
+// its barriers wait for the LDS only).
+template <class Sink, class Issue>
 __device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const float* __restrict__ w, float eps,
-                                             int n, float* sx, float* part, float* s_scale, Sink&& sink)
+                                             int n, float* sx, float* part, float* s_scale, Sink&& sink,
+                                             Issue&& issue)
 {
     const int tid = threadIdx.x;
     float* sq = sx + n;
@@ -313,22 +325,43 @@ __device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const
         wpre[i] = b < n / 32 ? *reinterpret_cast<const float4*>(w + 32 * b + 4 * l8) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (n & 3) == 0) {
-        // float4 row copy, the loads of a thread issued together; the squares x·x (rounded,
-        // as the reference's running sums add them) alongside
-#pragma unroll 4
-        for (int i = tid; i < n / 4; i += 256) {
+        // float4 row copy: a thread's first RPRE loads issued together (unconditionally, a
+        // load past the row re-reading its last float4, so no branch separates them), then
+        // issue(), then the copies and the squares x·x (rounded, as the reference's running
+        // sums add them); a longer row's remaining float4s load and store one by one
+        constexpr int RPRE = 4;
+        float4 rv[RPRE];
+#pragma unroll
+        for (int k = 0; k < RPRE; k++) {
+            const int i = tid + 256 * k;
+            rv[k] = reinterpret_cast<const float4*>(xr)[i < n / 4 ? i : n / 4 - 1];
+        }
+        asm volatile("" ::: "memory");
+        issue();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < RPRE; k++) {
+            const int i = tid + 256 * k;
+            if (i < n / 4) {
+                const float4 v = rv[k];
+                reinterpret_cast<float4*>(sx)[i] = v;
+                reinterpret_cast<float4*>(sq)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+            }
+        }
+        for (int i = tid + 256 * RPRE; i < n / 4; i += 256) {
             const float4 v = reinterpret_cast<const float4*>(xr)[i];
             reinterpret_cast<float4*>(sx)[i] = v;
             reinterpret_cast<float4*>(sq)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
         }
     } else {
+        issue();
         for (int i = tid; i < n; i += 256) {
             const float v = xr[i];
             sx[i] = v;
             sq[i] = v * v;
         }
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < 16) {
         // lane tid's running sum over elements tid + 16k in order; the reads of 16 steps are
         // issued together into one of two register sets, the next 16 (kept ahead by an empty
@@ -366,7 +399,7 @@ __device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const
         for (; k < nk; k++) acc = acc + sq[k * 16 + tid];
         part[tid] = acc;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid == 0) {
         double sum = 0.0;
         int i = 0;
@@ -377,7 +410,7 @@ __device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const
         for (; i < n; i++) sum += (double)sx[i] * (double)sx[i];
         *s_scale = 1.0f / sqrtf((float)(sum / n) + eps);
     }
-    __syncthreads();
+    lds_barrier();
     const float sc = *s_scale;
     int i = 0;
     for (int b = tid >> 3; b < n / 32; b += 256 >> 3, i++) {  // uniform per 8-lane group
@@ -416,7 +449,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
     rmsnorm_rows(x + (int64_t)t * ldx, w, eps, n, sx, part, &s_scale, [&](float4 v, int l8, int b) {
         if (y_row) *reinterpret_cast<float4*>(y_row + 32 * b + 4 * l8) = v;
         quant_block8(v, l8, a, t, b, 0);
-    });
+    }, [] {});
 }
 
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float eps, int n, const ActQ8& a,
@@ -1358,13 +1391,18 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     const int64_t rec0 = (int64_t)(row >> 5) * B;
     const int ri = row & 31;
 
+    // The first batch of weight loads is issued before the input is staged, or, when the
+    // work-group normalizes the hidden row itself, right after the row's loads: the RMSNorm
+    // then runs while the batch is in flight (its barriers wait for the LDS only).
     NarrowBatch<TYPE, NB> cur, nxt;
-    narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
+    if (!nin.x) narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
 
     if (nin.x) {
         // the codes formed here from the hidden rows: Kernels.RmsNorm, then the 32-block
         // quantization, into the arrays the staged codes would fill (the row's scratch follows)
-        float* nsx = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(sDs + NT * B) + 15) & ~(uintptr_t)15);
+        // (offset from the LDS base, so the pointer keeps the LDS address space)
+        const int nsx_off = (int)(reinterpret_cast<const char*>(sDs + NT * B) - reinterpret_cast<const char*>(nw_lds));
+        float* nsx = reinterpret_cast<float*>(reinterpret_cast<char*>(nw_lds) + ((nsx_off + 15) & ~15));
         uint8_t* sAb = reinterpret_cast<uint8_t*>(sA);
         const int K = 32 * B;
         for (int t = 0; t < NT; ++t) {
@@ -1379,8 +1417,11 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
                                  sSum[t * B + b] = qb.sum;
                                  sDs[t * B + b] = qb.d * (float)qb.sum;
                              }
+                         },
+                         [&] {
+                             if (t == 0) narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
                          });
-            __syncthreads();
+            lds_barrier();
         }
     } else {
         for (int i = tid; i < NT * B * 2; i += 256) {
