@@ -290,9 +290,10 @@ __device__ inline float vsum8(const float* a)
     return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
 }
 
-// A work-group barrier that waits only for this wave's LDS operations. Global loads in flight
-// (a caller's prefetched weights) stay in flight, where __syncthreads() (s_waitcnt vmcnt(0))
-// would wait for them; only LDS data may be handed between waves across it.
+// A work-group barrier that waits only for this wave's LDS operations, whatever else is
+// outstanding: global loads in flight (a caller's prefetched weights) stay in flight. The
+// fence of __syncthreads() also waits for every vector-memory operation once the wave has
+// generic (flat) accesses outstanding. Only LDS data may be handed between waves across it.
 __device__ __forceinline__ void lds_barrier()
 {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
