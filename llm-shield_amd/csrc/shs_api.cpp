@@ -1123,19 +1123,23 @@ shs_status run_head(shs_model* m, const std::vector<int32_t>& rows, int head_mod
 {
     const shs_config& c = m->cfg;
     const int n = (int)rows.size();
-    HIP_TRY(m->lastidx.ensure(sizeof(int32_t) * n));
-    HIP_TRY(m->last_rows.ensure(sizeof(float) * (size_t)n * c.hidden));
     HIP_TRY(m->normed.ensure(sizeof(float) * (size_t)std::max(n, 1) * c.hidden));
-    HIP_TRY(hipMemcpyAsync(m->lastidx.p, rows.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(launch_gather_rows(m->h.as<float>(), c.hidden, m->lastidx.as<int32_t>(), n, c.hidden, m->last_rows.as<float>(),
-                               c.hidden, m->stream));
+    // one row (a prompt's last token) is read in place; several are gathered first
+    const float* x_in = m->h.as<float>() + (n == 1 ? (size_t)rows[0] * c.hidden : 0);
+    if (n != 1) {
+        HIP_TRY(m->lastidx.ensure(sizeof(int32_t) * n));
+        HIP_TRY(m->last_rows.ensure(sizeof(float) * (size_t)n * c.hidden));
+        HIP_TRY(hipMemcpyAsync(m->lastidx.p, rows.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
+        HIP_TRY(launch_gather_rows(m->h.as<float>(), c.hidden, m->lastidx.as<int32_t>(), n, c.hidden,
+                                   m->last_rows.as<float>(), c.hidden, m->stream));
+        x_in = m->last_rows.as<float>();
+    }
     ActQ8 a;
     HIP_TRY(m->act.ensure(n, c.hidden, &a));
     float* normed = m->cap_fn ? m->normed.as<float>() : nullptr;
     {
         Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
-        HIP_TRY(launch_rmsnorm_quant(m->last_rows.as<float>(), c.hidden, m->out_norm, c.rms_eps, c.hidden, a, normed,
-                                     m->stream));
+        HIP_TRY(launch_rmsnorm_quant(x_in, c.hidden, m->out_norm, c.rms_eps, c.hidden, a, normed, m->stream));
     }
     Capture cp{m, {}};
     if (m->cap_fn && cp.observe("final_norm", normed, c.hidden, n, c.hidden) != SHS_OK) return SHS_E_DEVICE;
