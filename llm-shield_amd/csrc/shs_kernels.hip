@@ -325,7 +325,7 @@ __device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const
         const int b = (tid >> 3) + (256 >> 3) * i;
         wpre[i] = b < n / 32 ? *reinterpret_cast<const float4*>(w + 32 * b + 4 * l8) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    if (((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (n & 3) == 0) {
+    if (((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (n & 3) == 0 && n >= 4) {
         // float4 row copy: a thread's first RPRE loads issued together (unconditionally, a
         // load past the row re-reading its last float4, so no branch separates them), then
         // issue(), then the copies and the squares x·x (rounded, as the reference's running
