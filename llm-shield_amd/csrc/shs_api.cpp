@@ -74,6 +74,28 @@ struct Buf {
     template <class T> T* as() const { return static_cast<T*>(p); }
 };
 
+// Pinned host memory (hipHostMalloc), for the staging of small uploads.
+struct HostBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    ~HostBuf() { release(); }
+    void release()
+    {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    hipError_t ensure(size_t n)
+    {
+        if (n <= bytes) return hipSuccess;
+        release();
+        hipError_t e = hipHostMalloc(&p, n, hipHostMallocDefault);
+        if (e == hipSuccess) bytes = n;
+        else p = nullptr;
+        return e;
+    }
+};
+
 struct ActBuf {
     Buf q, d, cv, ds;
     hipError_t ensure(int T, int K, ActQ8* view)
@@ -356,6 +378,8 @@ struct shs_model {
     int64_t attn_pairs = 0;
     ActBuf act;
     ActBuf act_ffn;  // the fused gate|up GEMM's output codes (its input codes live in act)
+    HostBuf stage;   // pinned staging of a call's small uploads (upload())
+    size_t stage_used = 0;
     shs_capture_fn cap_fn = nullptr;
     void* cap_user = nullptr;
     Profiler prof;
@@ -1168,6 +1192,33 @@ std::vector<AttnItem> causal_items(int q_begin, int n, int key_start, int pos0)
     return v;
 }
 
+// A call's small uploads (token ids, positions, attention work) go through the pinned staging
+// buffer, so their copies are asynchronous and the call queues its kernels without waiting for
+// them. begin_uploads runs before a call's first upload and waits for the stream (idle then:
+// every call synchronizes before it returns, an early error return included the next call's
+// wait), so the buffer can be reused. An upload that does not fit is copied directly and
+// waited for.
+hipError_t begin_uploads(shs_model* m)
+{
+    hipError_t e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) return e;
+    m->stage_used = 0;
+    return m->stage.ensure(256u << 10);
+}
+
+hipError_t upload(shs_model* m, void* dst, const void* src, size_t bytes)
+{
+    if (bytes == 0) return hipSuccess;
+    if (m->stage.p && m->stage_used + bytes <= m->stage.bytes) {
+        char* st = static_cast<char*>(m->stage.p) + m->stage_used;
+        memcpy(st, src, bytes);
+        m->stage_used += (bytes + 255) & ~(size_t)255;
+        return hipMemcpyAsync(dst, st, bytes, hipMemcpyHostToDevice, m->stream);
+    }
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, m->stream);
+    return e != hipSuccess ? e : hipStreamSynchronize(m->stream);
+}
+
 // Gives every item its own region of the score scratch (4 waves per KV head, one 32×32
 // tile of 1024 floats per key tile), splits the items' key tiles into the score kernel's
 // chunks (longest items first, so they start first) and sizes the scratch: score tiles,
@@ -1215,13 +1266,10 @@ shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
     for (const auto& it : items) m->attn_pairs += (int64_t)it.q_count * it.pos0 + (int64_t)it.q_count * (it.q_count + 1) / 2;
     HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off + m->pm_floats, 1)));
     HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
-    HIP_TRY(hipMemcpyAsync(m->items.p, items.data(), sizeof(AttnItem) * items.size(), hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(upload(m, m->items.p, items.data(), sizeof(AttnItem) * items.size()));
     HIP_TRY(m->chunks.ensure(sizeof(AttnChunk) * std::max<size_t>(chunks.size(), 1)));
-    HIP_TRY(hipMemcpyAsync(m->chunks.p, chunks.data(), sizeof(AttnChunk) * chunks.size(), hipMemcpyHostToDevice,
-                           m->stream));
+    HIP_TRY(upload(m, m->chunks.p, chunks.data(), sizeof(AttnChunk) * chunks.size()));
     m->n_chunks = (int)chunks.size();
-    // The host vectors go out of scope: wait for the copies.
-    HIP_TRY(hipStreamSynchronize(m->stream));
     return SHS_OK;
 }
 
@@ -1250,12 +1298,13 @@ extern "C" shs_status shs_forward(shs_model* m, const int32_t* tokens, int32_t n
     std::vector<int32_t> pos(n);
     for (int t = 0; t < n; t++) pos[t] = start + t;
     std::vector<AttnItem> items = causal_items(0, n, 0, start);
+    HIP_TRY(begin_uploads(m));
     if ((st = place_items(m, items)) != SHS_OK) return st;
-    HIP_TRY(hipMemcpyAsync(m->tokens.p, tokens, sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(upload(m, m->tokens.p, tokens, sizeof(int32_t) * n));
+    HIP_TRY(upload(m, m->pos.p, pos.data(), sizeof(int32_t) * n));
     if (head_mode == 1) {
         HIP_TRY(m->ids.ensure(sizeof(int32_t) * n_ids));
-        HIP_TRY(hipMemcpyAsync(m->ids.p, vocab_ids, sizeof(int32_t) * n_ids, hipMemcpyHostToDevice, m->stream));
+        HIP_TRY(upload(m, m->ids.p, vocab_ids, sizeof(int32_t) * n_ids));
     }
     {
         Timed tm(m->prof, "embed", 0, m->stream);
@@ -1316,11 +1365,12 @@ extern "C" shs_status shs_forward_batch(shs_model* m, const int32_t* tokens, con
     // The kernel takes items from the back: put the longest key ranges there.
     std::stable_sort(items.begin(), items.end(),
                      [](const AttnItem& x, const AttnItem& y) { return x.pos0 + x.q_count < y.pos0 + y.q_count; });
+    HIP_TRY(begin_uploads(m));
     if ((st = place_items(m, items)) != SHS_OK) return st;
     HIP_TRY(m->ids.ensure(sizeof(int32_t) * n_ids));
-    HIP_TRY(hipMemcpyAsync(m->tokens.p, tokens, sizeof(int32_t) * T, hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * T, hipMemcpyHostToDevice, m->stream));
-    HIP_TRY(hipMemcpyAsync(m->ids.p, vocab_ids, sizeof(int32_t) * n_ids, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(upload(m, m->tokens.p, tokens, sizeof(int32_t) * T));
+    HIP_TRY(upload(m, m->pos.p, pos.data(), sizeof(int32_t) * T));
+    HIP_TRY(upload(m, m->ids.p, vocab_ids, sizeof(int32_t) * n_ids));
     {
         Timed tm(m->prof, "embed", 0, m->stream);
         HIP_TRY(launch_embed(m->embd, m->tokens.as<int32_t>(), T, m->h.as<float>(), c.hidden, m->stream));
@@ -1354,8 +1404,9 @@ extern "C" shs_status shs_layer_forward(shs_model* m, int32_t layer, const float
     std::vector<int32_t> pos(n);
     for (int t = 0; t < n; t++) pos[t] = t;
     std::vector<AttnItem> items = causal_items(0, n, 0, 0);
+    HIP_TRY(begin_uploads(m));
     if ((st = place_items(m, items)) != SHS_OK) return st;
-    HIP_TRY(hipMemcpyAsync(m->pos.p, pos.data(), sizeof(int32_t) * n, hipMemcpyHostToDevice, m->stream));
+    HIP_TRY(upload(m, m->pos.p, pos.data(), sizeof(int32_t) * n));
     HIP_TRY(hipMemcpyAsync(m->h.p, x, sizeof(float) * (size_t)n * c.hidden, hipMemcpyHostToDevice, m->stream));
     m->len = 0;
     st = run_layers(m, n, m->kc, m->vc, m->cap, 0, layer, layer + 1, m->items.as<AttnItem>(), (int)items.size(), nullptr, true);
