@@ -135,6 +135,12 @@ def test_selected_rows_are_bit_identical_to_the_full_head(shs, tiny):
     gpu.reset_kv_cache()
     sel = gpu.forward_selected(toks, ids)
     assert np.array_equal(sel, full[ids])
+    # 70000 ids (280 KB) do not fit the library's pinned upload staging: that upload takes the
+    # direct, waited copy, and the rows are still the full head's
+    many = np.random.default_rng(3).integers(0, cfg.vocab, 70000)
+    gpu.reset_kv_cache()
+    sel = gpu.forward_selected(toks, many)
+    assert np.array_equal(sel, full[many])
 
 
 def test_single_token_decode_matches_the_oracle(shs, tiny):
