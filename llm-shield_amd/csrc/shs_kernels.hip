@@ -1395,36 +1395,15 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
     // The first batch of weight loads is issued before the input is staged, or, when the
     // work-group normalizes the hidden row itself, right after the row's loads: the RMSNorm
     // then runs while the batch is in flight (its barriers wait for the LDS only).
+    // (only the q|k|v and gate|up launches normalize their own input; the other modes are
+    // compiled without that path)
+    constexpr bool NORM_MODE = MODE == GEMM_QKV || MODE == GEMM_SWIGLU;
+    const bool norm_in = NORM_MODE && nin.x != nullptr;
     NarrowBatch<TYPE, NB> cur, nxt;
-    if (!nin.x) narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
+    if (!norm_in) narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
 
-    if (nin.x) {
-        // the codes formed here from the hidden rows: Kernels.RmsNorm, then the 32-block
-        // quantization, into the arrays the staged codes would fill (the row's scratch follows)
-        // (offset from the LDS base, so the pointer keeps the LDS address space)
-        const int nsx_off = (int)(reinterpret_cast<const char*>(sDs + NT * B) - reinterpret_cast<const char*>(nw_lds));
-        float* nsx = reinterpret_cast<float*>(reinterpret_cast<char*>(nw_lds) + ((nsx_off + 15) & ~15));
-        uint8_t* sAb = reinterpret_cast<uint8_t*>(sA);
-        const int K = 32 * B;
-        for (int t = 0; t < NT; ++t) {
-            rmsnorm_rows(nin.x + (int64_t)t * nin.ldx, nin.w, nin.eps, K, nsx, nsx + 2 * K, nsx + 2 * K + 16,
-                         [&](float4 v, int l8, int b) {
-                             const QBlock qb = quant_block8_values(v, 0);
-                             // element group 4·l8 .. +3 sits in half (l8 >> 1) & 1 (the act_code_offset order)
-                             const int hf = (l8 >> 1) & 1, idx = 4 * (l8 & 1) + 8 * (l8 >> 2);
-                             *reinterpret_cast<uint32_t*>(sAb + ((t * B + b) * 2 + hf) * 16 + idx) = qb.w;
-                             if (l8 == 0) {
-                                 sDa[t * B + b] = qb.d;
-                                 sSum[t * B + b] = qb.sum;
-                                 sDs[t * B + b] = qb.d * (float)qb.sum;
-                             }
-                         },
-                         [&] {
-                             if (t == 0) narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
-                         });
-            lds_barrier();
-        }
-    } else {
+    // the staged input: codes, d_a and Σa of the NT tokens from the activation buffers
+    auto stage_codes = [&] {
         for (int i = tid; i < NT * B * 2; i += 256) {
             const int t = i / (2 * B), rem = i - t * 2 * B, b = rem >> 1, h = rem & 1;
             sA[i] = *reinterpret_cast<const uint4*>(a.q + (((int64_t)(t >> 5) * B + b) * 64 + (t & 31)) * 16 + h * 512);
@@ -1443,10 +1422,42 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
             }
         }
         __syncthreads();
+    };
+    if constexpr (NORM_MODE) {
+        if (norm_in) {
+            // the codes formed here from the hidden rows: Kernels.RmsNorm, then the 32-block
+            // quantization, into the arrays the staged codes would fill (the row's scratch follows)
+            // (offset from the LDS base, so the pointer keeps the LDS address space)
+            const int nsx_off = (int)(reinterpret_cast<const char*>(sDs + NT * B) - reinterpret_cast<const char*>(nw_lds));
+            float* nsx = reinterpret_cast<float*>(reinterpret_cast<char*>(nw_lds) + ((nsx_off + 15) & ~15));
+            uint8_t* sAb = reinterpret_cast<uint8_t*>(sA);
+            const int K = 32 * B;
+            for (int t = 0; t < NT; ++t) {
+                rmsnorm_rows(nin.x + (int64_t)t * nin.ldx, nin.w, nin.eps, K, nsx, nsx + 2 * K, nsx + 2 * K + 16,
+                             [&](float4 v, int l8, int b) {
+                                 const QBlock qb = quant_block8_values(v, 0);
+                                 // element group 4·l8 .. +3 sits in half (l8 >> 1) & 1 (the act_code_offset order)
+                                 const int hf = (l8 >> 1) & 1, idx = 4 * (l8 & 1) + 8 * (l8 >> 2);
+                                 *reinterpret_cast<uint32_t*>(sAb + ((t * B + b) * 2 + hf) * 16 + idx) = qb.w;
+                                 if (l8 == 0) {
+                                     sDa[t * B + b] = qb.d;
+                                     sSum[t * B + b] = qb.sum;
+                                     sDs[t * B + b] = qb.d * (float)qb.sum;
+                                 }
+                             },
+                             [&] {
+                                 if (t == 0) narrow_load<TYPE, R, NB>(cur, wqs, wqh, wd, wm, rec0, ri, bl, B);
+                             });
+                lds_barrier();
+            }
+        } else {
+            stage_codes();
+        }
+    } else {
+        stage_codes();
     }
 
-    // batches of NB·BS blocks; the next batch is prefetched only when there is one (a barrier
-    // waits for every load in flight)
+    // batches of NB·BS blocks; the next batch is prefetched only when there is one
     const int n_batch = (B + NB * BS - 1) / (NB * BS);
     for (int bt = 0; bt < n_batch; bt++) {
         const int b0 = bl + bt * NB * BS;
