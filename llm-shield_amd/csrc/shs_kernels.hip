@@ -698,7 +698,11 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, h = lane >> 5;
     const int R = xcd_order(blockIdx.x, gridDim.x);
-    const int rg = R / n_tg, tg = R - rg * n_tg;
+    // token groups fastest (an XCD's work-groups share a few row groups' weights in its L2);
+    // the one-round q|k|v launch measured faster with row groups fastest
+    const int n_rg = gridDim.x / n_tg;
+    const int rg = MODE == GEMM_QKV ? R % n_rg : R / n_tg;
+    const int tg = MODE == GEMM_QKV ? R / n_rg : R - rg * n_tg;
     // GEMM_SWIGLU: waves 0/1 take gate/up of feature tile 2·rg, waves 2/3 of 2·rg + 1
     const int ft = 2 * rg + (wave >> 1);
     const int rt = MODE == GEMM_SWIGLU ? (wave & 1) * n_ft + ft : rg * 4 + wave;
