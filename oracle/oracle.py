@@ -95,6 +95,7 @@ def _declare(L: C.CDLL) -> None:
     L.ora_score.argtypes = [P, C.c_int, C.c_int, P, P, P]
     L.ora_expf.argtypes = [C.c_float]
     L.ora_expf.restype = C.c_float
+    L.ora_expf_n.argtypes = [P, C.c_int64, P]
     L.ora_layer_forward.argtypes = [C.POINTER(Model), C.POINTER(KV), C.c_int, P, C.c_int, P, C.c_int]
 
 
@@ -197,6 +198,14 @@ def swiglu(g, u):
     out = np.empty_like(g)
     lib().ora_swiglu(_p(g), _p(u), _p(out), g.size)
     return out
+
+
+def expf(x):
+    """ora_expf elementwise."""
+    x = _c(x, np.float32).reshape(-1)
+    y = np.empty_like(x)
+    lib().ora_expf_n(_p(x), x.size, _p(y))
+    return y
 
 
 def softmax(x):

@@ -63,6 +63,7 @@ int ora_gather_rows(int type, const uint8_t* table, int rows, int cols,
 /* ------------------------------------------------------------ elementwise */
 void ora_rmsnorm(const float* x, const float* w, float eps, int n, float* y);      /* Kernels.cs:26-61 */
 float ora_expf(float x);                                                          /* TensorPrimitives.Exp */
+void ora_expf_n(const float* x, int64_t n, float* y);
 void ora_swiglu(const float* gate, float* up, float* dst, int64_t n);              /* Kernels.cs:83-90 */
 void ora_softmax(float* x, int n);                                                 /* Kernels.cs:103-122 */
 void ora_dot4(const float* shared, const float* a0, const float* a1, const float* a2,

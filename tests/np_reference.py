@@ -69,18 +69,64 @@ def rmsnorm(x, g, eps):
     return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(g, np.float64)
 
 
-def rope(x, heads, hd, pos, theta, rope_dim):
+def rope_freqs(cfg):
+    """Rotary frequencies and magnitude factor in float64 (Rope.cs:33-106): plain
+    1/θ^(2i/d)/factor, or YaRN's ramp between the interpolated and extrapolated
+    frequencies with ggml's correction dimensions and the mscale ratio."""
+    d = cfg.rope_dim
+    half = d // 2
+    i = np.arange(half, dtype=np.float64)
+    ext = 1.0 / cfg.rope_theta ** (2.0 * i / d)
+    factor = float(cfg.rope_scale)
+    if not cfg.yarn_active:
+        return ext / factor, float(cfg.rope_attn_factor)
+    bf, bs = float(cfg.yarn_beta_fast), float(cfg.yarn_beta_slow)
+
+    def corr(rot):
+        return d * np.log(cfg.rope_orig_ctx / (rot * 2 * np.pi)) / (2 * np.log(cfg.rope_theta))
+
+    if bf == 0 and bs == 0:
+        low, high = np.inf, half - 1.0
+    else:
+        low, high = max(0.0, np.floor(corr(bf))), min(half - 1.0, np.ceil(corr(bs)))
+    ramp = np.clip((i - low) / max(0.001, high - low), 0.0, 1.0)
+    mix = (1.0 - ramp) * cfg.yarn_ext_factor
+    freqs = ext / factor * (1.0 - mix) + ext * mix
+
+    def msc(m):
+        return 1.0 if factor <= 1 else 0.1 * m * np.log(factor) + 1.0
+
+    m = cfg.yarn_mscale if cfg.yarn_mscale != 0 else 1.0
+    ratio = msc(m) / msc(cfg.yarn_mscale_all_dim) if cfg.yarn_mscale_all_dim != 0 else msc(1.0)
+    return freqs, ratio * cfg.rope_attn_factor
+
+
+def query_temperature(cfg, pos):
+    """Llama-4 attention temperature per position (MinistralModel.cs:471-482)."""
+    pos = np.asarray(pos, np.float64)
+    if cfg.rope_orig_ctx <= 0 or cfg.attn_temperature == 0:
+        return np.ones_like(pos)
+    return 1.0 + cfg.attn_temperature * np.log1p(np.floor(pos / cfg.rope_orig_ctx))
+
+
+def rope(x, heads, hd, pos, theta, rope_dim, freqs=None, mscale=1.0):
     """Adjacent-pair rotation; x [T, heads·hd]; pos [T]."""
     T = x.shape[0]
     half = rope_dim // 2
-    freq = 1.0 / theta ** (2.0 * np.arange(half) / rope_dim)
+    freq = 1.0 / theta ** (2.0 * np.arange(half) / rope_dim) if freqs is None else np.asarray(freqs, np.float64)
     ang = np.asarray(pos, np.float64)[:, None] * freq[None, :]
-    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    c, s = mscale * np.cos(ang)[:, None, :], mscale * np.sin(ang)[:, None, :]
     y = np.array(x, np.float64).reshape(T, heads, hd)
     x0, x1 = y[:, :, 0:rope_dim:2].copy(), y[:, :, 1:rope_dim:2].copy()
     y[:, :, 0:rope_dim:2] = x0 * c - x1 * s
     y[:, :, 1:rope_dim:2] = x0 * s + x1 * c
     return y.reshape(T, heads * hd)
+
+
+def swiglu(g, u):
+    """Kernels.SwiGlu (Kernels.cs:83-90) in float64: sigmoid(g)·(g·u)."""
+    g = np.asarray(g, np.float64)
+    return g * np.asarray(u, np.float64) / (1.0 + np.exp(-g))
 
 
 def attention(q, k, v, n_head, n_kv, hd, q_pos, k_pos):
@@ -112,20 +158,22 @@ def forward(cfg, tensors, types, tokens, head="full", vocab_ids=None, layers=Non
     emb = dequantize(types["token_embd.weight"], tensors["token_embd.weight"], cfg.vocab, cfg.hidden)
     h = emb[toks].astype(np.float64)
     pos = np.arange(T)
+    freqs, ms = rope_freqs(cfg)
+    temp = query_temperature(cfg, pos)[:, None]
     for l in range(L if layers is None else layers):
         p = f"blk.{l}."
         x = rmsnorm(h, tensors[p + "attn_norm.weight"], cfg.eps)
         q = qmatmul(types[p + "attn_q.weight"], tensors[p + "attn_q.weight"], qd, cfg.hidden, x)
         k = qmatmul(types[p + "attn_k.weight"], tensors[p + "attn_k.weight"], kvd, cfg.hidden, x)
         v = qmatmul(types[p + "attn_v.weight"], tensors[p + "attn_v.weight"], kvd, cfg.hidden, x)
-        q = rope(q, H, hd, pos, cfg.rope_theta, cfg.rope_dim)
-        k = rope(k, KV, hd, pos, cfg.rope_theta, cfg.rope_dim)
+        q = rope(q, H, hd, pos, cfg.rope_theta, cfg.rope_dim, freqs, ms) * temp
+        k = rope(k, KV, hd, pos, cfg.rope_theta, cfg.rope_dim, freqs, ms)
         ctx = attention(q, k, v, H, KV, hd, pos, pos)
         h = h + qmatmul(types[p + "attn_output.weight"], tensors[p + "attn_output.weight"], cfg.hidden, qd, ctx)
         x = rmsnorm(h, tensors[p + "ffn_norm.weight"], cfg.eps)
         g = qmatmul(types[p + "ffn_gate.weight"], tensors[p + "ffn_gate.weight"], cfg.ffn, cfg.hidden, x)
         u = qmatmul(types[p + "ffn_up.weight"], tensors[p + "ffn_up.weight"], cfg.ffn, cfg.hidden, x)
-        a = g / (1.0 + np.exp(-g)) * u
+        a = swiglu(g, u)
         h = h + qmatmul(types[p + "ffn_down.weight"], tensors[p + "ffn_down.weight"], cfg.hidden, cfg.ffn, a)
     if head is None:
         return h
