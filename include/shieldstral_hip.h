@@ -50,6 +50,8 @@ typedef struct {
     float   yarn_mscale, yarn_mscale_all_dim, rope_attn_factor;
     float   attn_temperature; /* Llama-4 attention temperature beta, 0 = off */
     int32_t yarn_active;      /* ModelConfig.YarnActive (ModelConfig.cs:54-56) */
+    char    architecture[32]; /* ModelConfig.Architecture (ModelConfig.cs:14,77): general.architecture,
+                                 NUL-terminated; empty on input means "mistral3" */
 } shs_config;
 
 /* One named tensor in its native GGUF block layout, shape [ne0 = in, ne1 = out]
@@ -81,6 +83,10 @@ shs_status shs_open_tensors(const shs_config* cfg, const shs_tensor* tensors, in
  * file (GgufFile.cs:76-199), reads ModelConfig (ModelConfig.cs:62-112) and calls
  * shs_open_tensors. The mapping is released before returning. */
 shs_status shs_open(const char* gguf_path, int32_t device, int32_t initial_capacity, shs_model** out);
+
+/* ModelConfig.FromGguf (ModelConfig.cs:62-112) on a GGUF file's header, after GgufFile's
+ * header parse and truncation check (GgufFile.cs:110-172); touches no device. */
+shs_status shs_read_config(const char* gguf_path, shs_config* out);
 
 /* A random-init model of cfg's shape built directly in HBM, for benchmarks and tests
  * (no counterpart in the reference, which only loads converted checkpoints; its

@@ -653,6 +653,8 @@ shs_status build_model(const shs_config& c, const SpecMap& tm, int device, int i
     if ((st = select_device(device)) != SHS_OK) return st;
     shs_model* m = new shs_model();
     m->cfg = c;
+    m->cfg.architecture[sizeof m->cfg.architecture - 1] = 0;
+    if (!m->cfg.architecture[0]) snprintf(m->cfg.architecture, sizeof m->cfg.architecture, "mistral3");
     m->device = device;
     auto bail = [&](shs_status s) {
         std::string keep = g_error;

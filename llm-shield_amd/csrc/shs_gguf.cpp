@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstring>
 #include <map>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -36,9 +37,11 @@ struct Reader {
     const uint8_t* p;
     size_t n, pos = 0;
     bool ok = true;
-    bool need(size_t k)
+    // pos <= n always holds, so n - pos cannot wrap; pos + k could (a 64-bit string
+    // length near 2^64 from a damaged header).
+    bool need(uint64_t k)
     {
-        if (!ok || pos + k > n) ok = false;
+        if (!ok || k > n - pos) ok = false;
         return ok;
     }
     template <class T> T get()
@@ -115,10 +118,14 @@ shs_status err(shs_status code, const char* fmt, ...)
 
 }  // namespace
 
-extern "C" shs_status shs_open(const char* path, int32_t device, int32_t initial_capacity, shs_model** out)
+// Reads the file's header and ModelConfig; with out == nullptr it stops there (after
+// the truncation check, as GgufFile's constructor runs it before FromGguf) and reports
+// the config through cfg_out, else it uploads the tensors.
+static shs_status open_gguf(const char* path, int32_t device, int32_t initial_capacity, shs_model** out,
+                            shs_config* cfg_out)
 {
-    if (!path || !out) return err(SHS_E_INVALID_ARGUMENT, "null argument");
-    *out = nullptr;
+    if (!path || (!out && !cfg_out)) return err(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (out) *out = nullptr;
     int fd = open(path, O_RDONLY);
     if (fd < 0) return err(SHS_E_IO, "%s: cannot open (%s)", path, strerror(errno));
     struct stat sb;
@@ -159,8 +166,19 @@ extern "C" shs_status shs_open(const char* path, int32_t device, int32_t initial
     if (!r.ok) return err(SHS_E_IO, "%s is truncated inside its header; re-download it", path);
     uint64_t align = 32;
     auto ai = kv.find("general.alignment");
-    if (ai != kv.end() && ai->second.num > 0) align = (uint64_t)ai->second.num;
+    if (ai != kv.end()) {
+        double v = ai->second.num;
+        bool numeric = ai->second.type != STR && ai->second.type != ARR;
+        if (!numeric || !(v >= 1.0) || v > (double)map.size || v != (double)(uint64_t)v)
+            return err(SHS_E_INVALID_DATA, "%s has general.alignment %g; it must be a whole number from 1 to the file "
+                                           "size. Re-download the file.", path, v);
+        align = (uint64_t)v;
+    }
+    // r.pos <= map.size and align <= map.size, so neither the sum nor the product wraps.
     uint64_t data_off = (r.pos + align - 1) / align * align;
+    if (data_off > map.size)
+        return err(SHS_E_IO, "%s is truncated: its tensor data would start past the end of the file; re-download it",
+                   path);
 
     auto num = [&](const std::string& k, double dflt, bool* found = nullptr) {
         auto it = kv.find(k);
@@ -180,6 +198,7 @@ extern "C" shs_status shs_open(const char* path, int32_t device, int32_t initial
     const std::string a = arch + ".";
     bool found = false;
     shs_config c{};
+    snprintf(c.architecture, sizeof c.architecture, "%s", arch.c_str());
     c.n_head = (int)num(a + "attention.head_count", 0, &found);
     if (!found) return err(SHS_E_KEY_NOT_FOUND, "%s has no %sattention.head_count", path, a.c_str());
     c.hidden = (int)num(a + "embedding_length", 0, &found);
@@ -210,25 +229,34 @@ extern "C" shs_status shs_open(const char* path, int32_t device, int32_t initial
         return err(SHS_E_INVALID_DATA, "%d attention heads do not divide into %d KV heads.", c.n_head, c.n_kv_head);
 
     // Tensor table → shs_tensor, with GgufFile's truncation check (GgufFile.cs:156-172).
-    auto type_bytes = [](uint32_t t, uint64_t n) -> int64_t {
+    // Byte size of n elements, or false for a type this reader does not size (the
+    // reference skips those too) or a size that does not fit 64 bits.
+    auto type_bytes = [](uint32_t t, uint64_t n, uint64_t* out) -> bool {
+        uint64_t per, group;
         switch (t) {
-        case 0: return (int64_t)n * 4;
-        case 1: return (int64_t)n * 2;
-        case 2: return (int64_t)(n / 32) * 18;
-        case 3: return (int64_t)(n / 32) * 20;
-        case 6: return (int64_t)(n / 32) * 22;
-        case 7: return (int64_t)(n / 32) * 24;
-        case 8: return (int64_t)(n / 32) * 34;
-        default: return -1;
+        case 0: per = 4; group = 1; break;
+        case 1: per = 2; group = 1; break;
+        case 2: per = 18; group = 32; break;
+        case 3: per = 20; group = 32; break;
+        case 6: per = 22; group = 32; break;
+        case 7: per = 24; group = 32; break;
+        case 8: per = 34; group = 32; break;
+        default: return false;
         }
+        return !__builtin_mul_overflow(n / group, per, out);
     };
+    const uint64_t room = map.size - data_off;  // bytes from the data section to the end
     std::vector<shs_tensor> ts;
     ts.reserve(infos.size());
     for (auto& ti : infos) {
         uint64_t count = 1;
-        for (auto d : ti.dims) count *= d;
-        int64_t bytes = type_bytes(ti.type, count);
-        if (bytes >= 0 && data_off + ti.offset + (uint64_t)bytes > map.size)
+        bool huge = false;
+        for (auto d : ti.dims) huge |= __builtin_mul_overflow(count, d, &count);
+        if (huge || ti.offset > room)
+            return err(SHS_E_IO, "%s is truncated or damaged: tensor '%s' starts past the end of the file; "
+                                 "re-download it", path, ti.name.c_str());
+        uint64_t bytes = 0;
+        if (type_bytes(ti.type, count, &bytes) && bytes > room - ti.offset)
             return err(SHS_E_IO, "%s is truncated: tensor '%s' ends past the end of the file; re-download it", path,
                        ti.name.c_str());
         shs_tensor t{};
@@ -239,5 +267,35 @@ extern "C" shs_status shs_open(const char* path, int32_t device, int32_t initial
         t.data = static_cast<const uint8_t*>(map.base) + data_off + ti.offset;
         ts.push_back(t);
     }
+    if (!out) {
+        *cfg_out = c;
+        return SHS_OK;
+    }
     return shs_open_tensors(&c, ts.data(), (int32_t)ts.size(), device, initial_capacity, out);
+}
+
+// No C++ exception may cross the C ABI: an allocation that fails while the header is
+// parsed becomes a status.
+static shs_status guarded(const char* path, int32_t device, int32_t initial_capacity, shs_model** out,
+                          shs_config* cfg_out)
+{
+    try {
+        return open_gguf(path, device, initial_capacity, out, cfg_out);
+    } catch (const std::bad_alloc&) {
+        return err(SHS_E_IO, "%s: out of host memory while reading its header", path ? path : "(null)");
+    } catch (...) {
+        return err(SHS_E_INVALID_DATA, "%s: its header could not be read; re-download it", path ? path : "(null)");
+    }
+}
+
+extern "C" shs_status shs_open(const char* path, int32_t device, int32_t initial_capacity, shs_model** out)
+{
+    if (!out) return err(SHS_E_INVALID_ARGUMENT, "null argument");
+    return guarded(path, device, initial_capacity, out, nullptr);
+}
+
+extern "C" shs_status shs_read_config(const char* path, shs_config* out)
+{
+    if (!out) return err(SHS_E_INVALID_ARGUMENT, "null argument");
+    return guarded(path, 0, 0, nullptr, out);
 }

@@ -87,7 +87,7 @@ class shs_config(C.Structure):
         ("rope_scale", C.c_float), ("rope_orig_ctx", C.c_int32),
         ("yarn_beta_fast", C.c_float), ("yarn_beta_slow", C.c_float), ("yarn_ext_factor", C.c_float),
         ("yarn_mscale", C.c_float), ("yarn_mscale_all_dim", C.c_float), ("rope_attn_factor", C.c_float),
-        ("attn_temperature", C.c_float), ("yarn_active", C.c_int32),
+        ("attn_temperature", C.c_float), ("yarn_active", C.c_int32), ("architecture", C.c_char * 32),
     ]
 
 
@@ -99,7 +99,8 @@ CAPTURE_FN = C.CFUNCTYPE(None, C.c_char_p, C.POINTER(C.c_float), C.c_int32, C.c_
 
 #: Every symbol include/shieldstral_hip.h declares.
 EXPORTS = (
-    "shs_last_error", "shs_open_tensors", "shs_open", "shs_open_synthetic", "shs_tensor_download", "shs_close",
+    "shs_last_error", "shs_open_tensors", "shs_open", "shs_read_config", "shs_open_synthetic", "shs_tensor_download",
+    "shs_close",
     "shs_get_config", "shs_kv_reset", "shs_kv_length", "shs_kv_capacity", "shs_kv_snapshot", "shs_kv_restore",
     "shs_forward", "shs_forward_batch", "shs_set_capture", "shs_layer_forward", "shs_matrix_create",
     "shs_matrix_free", "shs_matmul", "shs_matmul_rows", "shs_matmul_block_sums", "shs_matmul_device",
@@ -133,6 +134,7 @@ def _declare(L: C.CDLL) -> None:
     sigs = {
         "shs_open_tensors": [C.POINTER(shs_config), C.POINTER(shs_tensor), I32, I32, I32, PP],
         "shs_open": [C.c_char_p, I32, I32, PP],
+        "shs_read_config": [C.c_char_p, C.POINTER(shs_config)],
         "shs_open_synthetic": [C.POINTER(shs_config), I32, I32, C.c_uint64, I32, I32, PP],
         "shs_tensor_download": [P, C.c_char_p, P, C.c_size_t],
         "shs_get_config": [P, C.POINTER(shs_config)],
@@ -205,6 +207,7 @@ class ModelConfig:
     rope_attn_factor: float = 1.0
     attention_temperature_scale: float = 0.0
     yarn_active: bool = False
+    architecture: str = "mistral3"
 
     @property
     def group_size(self) -> int:
@@ -228,13 +231,23 @@ class ModelConfig:
         c.yarn_mscale, c.yarn_mscale_all_dim = self.yarn_mscale, self.yarn_mscale_all_dim
         c.rope_attn_factor, c.attn_temperature = self.rope_attn_factor, self.attention_temperature_scale
         c.yarn_active = int(self.yarn_active)
+        c.architecture = self.architecture.encode()[:31]
         return c
 
     @classmethod
     def from_c(cls, c: shs_config) -> "ModelConfig":
         return cls(c.n_layer, c.hidden, c.n_head, c.n_kv_head, c.head_dim, c.ffn, c.vocab, c.rms_eps, c.rope_theta,
                    c.rope_dim, c.rope_scale, c.rope_orig_ctx, c.yarn_beta_fast, c.yarn_beta_slow, c.yarn_ext_factor,
-                   c.yarn_mscale, c.yarn_mscale_all_dim, c.rope_attn_factor, c.attn_temperature, bool(c.yarn_active))
+                   c.yarn_mscale, c.yarn_mscale_all_dim, c.rope_attn_factor, c.attn_temperature, bool(c.yarn_active),
+                   c.architecture.decode() or "mistral3")
+
+    @classmethod
+    def from_gguf(cls, gguf_path) -> "ModelConfig":
+        """ModelConfig.FromGguf (ModelConfig.cs:62-112): the header alone, no device."""
+        lib = load_library()
+        c = shs_config()
+        _check(lib.shs_read_config(str(gguf_path).encode(), C.byref(c)))
+        return cls.from_c(c)
 
     def tensor_shapes(self, weight_type: int, embd_type: int):
         """GGUF tensor table (MinistralModel.cs:74-96): name → (type, ne0, ne1)."""
@@ -624,7 +637,8 @@ class SystemPromptCache:
         else:
             ident = f"{os.path.basename(path)}|-1|-1|"
         c = model.config
-        s = ident + f"mistral3|{c.layer_count}x{c.kv_head_count}x{c.head_dim}|{len(toks)}:" + "".join(f"{t}," for t in toks)
+        s = (ident + f"{c.architecture}|{c.layer_count}x{c.kv_head_count}x{c.head_dim}|{len(toks)}:"
+             + "".join(f"{t}," for t in toks))
         return hashlib.sha256(s.encode()).hexdigest()
 
     @classmethod
@@ -688,7 +702,10 @@ class SystemPromptCache:
             (count,) = struct.unpack("<i", r.read(4))
             if count < 0 or count > 1_000_000:
                 return None
-            tokens = np.frombuffer(r.read(4 * count), "<i4").astype(np.int32)
+            raw_tokens = r.read(4 * count)
+            if len(raw_tokens) != 4 * count:
+                return None
+            tokens = np.frombuffer(raw_tokens, "<i4").astype(np.int32)
             (length,) = struct.unpack("<q", r.read(8))
             if length < 0 or length > 2**31 - 1:
                 return None

@@ -8,6 +8,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+import helpers as H
+
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "shieldstral_hip.h"
 
@@ -105,3 +107,109 @@ def test_config_tensor_table_matches_the_reference_names(shs):
     assert t["blk.0.attn_q.weight"][1:] == (3072, 4096)
     assert t["blk.25.ffn_down.weight"][1:] == (9216, 3072)
     assert t["token_embd.weight"][1:] == (3072, 131072)
+
+
+# ------------------------------------------------------------ GGUF header (CPU)
+
+def _tiny_gguf(oracle, tmp_path, name="m.gguf", arch="mistral3", cfg_kw=None, **kw):
+    import gguf_writer as GW
+    cfg = oracle.make_config(n_layer=1, hidden=64, n_head=2, n_kv_head=1, head_dim=32, ffn=96, vocab=64,
+                             rope_dim=32, **(cfg_kw or {}))
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=1)
+    path = tmp_path / name
+    GW.write_gguf(path, arch, cfg, tensors, types, **kw)
+    return path, cfg
+
+
+def test_read_config_follows_model_config_from_gguf(shs, oracle, tmp_path):
+    """ModelConfig.FromGguf on the header alone: hyperparameters, the architecture
+    string, and the converter's YaRN + temperature keys (YarnActive)."""
+    import gguf_writer as GW
+    yarn = dict(rope_scale=16.0, rope_orig_ctx=16, yarn_active=1, yarn_beta_fast=32.0, yarn_beta_slow=1.0,
+                yarn_mscale=1.0, yarn_mscale_all_dim=1.0, attn_temperature=0.1)
+    plain, _ = _tiny_gguf(oracle, tmp_path)
+    c = shs.ModelConfig.from_gguf(plain)
+    assert (c.layer_count, c.hidden_size, c.head_count, c.kv_head_count, c.head_dim) == (1, 64, 2, 1, 32)
+    assert c.vocab_size == 64 and c.architecture == "mistral3" and not c.yarn_active
+    cfg = oracle.make_config(n_layer=1, hidden=64, n_head=2, n_kv_head=1, head_dim=32, ffn=96, vocab=64,
+                             rope_dim=32, **yarn)
+    path, _ = _tiny_gguf(oracle, tmp_path, "y.gguf", arch="ministral3", cfg_kw=yarn,
+                         extra_kv=GW.yarn_keys("ministral3", cfg))
+    y = shs.ModelConfig.from_gguf(path)
+    assert y.architecture == "ministral3" and y.yarn_active
+    assert (y.rope_scale_factor, y.rope_original_context_length) == (16.0, 16)
+    assert (y.yarn_mscale, y.yarn_mscale_all_dim) == (1.0, 1.0)
+    assert y.attention_temperature_scale == pytest.approx(0.1)
+    assert (y.yarn_beta_fast, y.yarn_beta_slow, y.yarn_ext_factor, y.rope_attn_factor) == (32.0, 1.0, 1.0, 1.0)
+
+
+def test_damaged_headers_are_rejected_without_crashing(shs, oracle, tmp_path):
+    """A string length near 2^64, a tensor offset that would wrap past the end of the
+    address space, a fractional or zero general.alignment, and a header cut short: each
+    is an InvalidDataError or ModelIOError, never a crash (GgufFile.cs:110-172)."""
+    import struct as S
+    import gguf_writer as GW
+    good, _ = _tiny_gguf(oracle, tmp_path)
+    raw = bytearray(good.read_bytes())
+    # the first metadata key's length field sits right after the 24-byte header
+    bad = bytearray(raw)
+    bad[24:32] = S.pack("<Q", 2 ** 64 - 3)
+    p = tmp_path / "strlen.gguf"
+    p.write_bytes(bad)
+    with pytest.raises((shs.InvalidDataError, shs.ModelIOError)):
+        shs.ModelConfig.from_gguf(p)
+    for off in (2 ** 64 - 8, 2 ** 63, len(raw)):
+        p, _ = _tiny_gguf(oracle, tmp_path, f"off{off}.gguf", offset_override={"blk.0.ffn_down.weight": off})
+        with pytest.raises(shs.ModelIOError):
+            shs.ModelConfig.from_gguf(p)
+    for akv in ((GW.F32, 0.5), (GW.U32, 0), (GW.F32, 1.5), (GW.STR, "32")):
+        p, _ = _tiny_gguf(oracle, tmp_path, "align.gguf", alignment_kv=akv)
+        with pytest.raises(shs.InvalidDataError):
+            shs.ModelConfig.from_gguf(p)
+    for cut in (30, len(raw) // 3):
+        p = tmp_path / "cut.gguf"
+        p.write_bytes(raw[:cut])
+        with pytest.raises((shs.InvalidDataError, shs.ModelIOError)):
+            shs.ModelConfig.from_gguf(p)
+    p, _ = _tiny_gguf(oracle, tmp_path, "short.gguf", truncate_by=40)
+    with pytest.raises(shs.ModelIOError, match="truncated"):
+        shs.ModelConfig.from_gguf(p)
+    assert shs.ModelConfig.from_gguf(good).hidden_size == 64
+
+
+def test_shkv_fingerprint_carries_the_architecture(shs, oracle, tmp_path):
+    """ComputeFingerprint appends Config.Architecture (SystemPromptCache.cs:90-105): a
+    ministral3 GGUF's snapshot reloads against that model and its fingerprint is the
+    SHA-256 of the reference's string with "ministral3" in it."""
+    import hashlib
+    import os
+    path, _ = _tiny_gguf(oracle, tmp_path, "mini.gguf", arch="ministral3")
+    m = _FakeModel(shs, str(path))
+    m.config = shs.ModelConfig.from_gguf(path)
+    toks = np.array([5, 6, 7], np.int32)
+    fp = shs.SystemPromptCache.compute_fingerprint(m, toks)
+    st = os.stat(path)
+    ticks = st.st_mtime_ns // 100 + 621355968000000000
+    ref = f"mini.gguf|{st.st_size}|{ticks}|ministral3|1x1x32|3:5,6,7,"
+    assert fp == hashlib.sha256(ref.encode()).hexdigest()
+    state = np.arange(2 * 1 * 1 * 3 * 32, dtype=np.float32)
+    cache = shs.SystemPromptCache(toks, state, fp)
+    cache.save(tmp_path / "mini.shkv")
+    back = shs.SystemPromptCache.try_load(tmp_path / "mini.shkv", m)
+    assert back is not None and back.fingerprint == fp and np.array_equal(back.state, state)
+    m.config.architecture = "mistral3"
+    assert shs.SystemPromptCache.try_load(tmp_path / "mini.shkv", m) is None
+
+
+def test_shkv_truncated_inside_the_token_array_is_a_miss(shs, tmp_path):
+    """TryLoad returns null on EndOfStreamException (SystemPromptCache.cs:140-164), also
+    when the cut falls inside a token."""
+    m = _FakeModel(shs)
+    toks = np.arange(10, dtype=np.int32)
+    c = shs.SystemPromptCache(toks, np.zeros(8, np.float32), shs.SystemPromptCache.compute_fingerprint(m, toks))
+    c.save(tmp_path / "t.shkv")
+    raw = (tmp_path / "t.shkv").read_bytes()
+    start = 8 + 1 + 64 + 4
+    for cut in (start + 1, start + 6, start + 39):
+        (tmp_path / "t.shkv").write_bytes(raw[:cut])
+        assert shs.SystemPromptCache.try_load(tmp_path / "t.shkv", m) is None
