@@ -119,8 +119,32 @@ __device__ __forceinline__ uint32_t half_bits(int v)
 // fp16 (−6144, −hi, −lo, 0) with Σq = 64·hi + lo, 0 ≤ lo < 64, so |hi| ≤ 64 — every
 // entry an exact fp16 integer. Against the A row (2048, 64z, z, 0) it sums to
 // −(1.5·2^23 + z·Σq).
+// vcvtps2dq, the conversion IntegerGemm.QuantizeActivations uses: round to nearest even;
+// NaN and values outside the int32 range give 0x80000000 (v_cvt_i32_f32 alone would
+// saturate instead).
+__device__ __forceinline__ int cvt_rne_x86(float v)
+{
+    const float r = __builtin_rintf(v);
+    return __builtin_fabsf(r) < 2147483648.0f ? (int)r : (int)0x80000000;
+}
+
+// The code a converted value packs to (vpackssdw + vpacksswb: signed saturation).
+__device__ __forceinline__ uint32_t code_byte(int q)
+{
+    return (uint32_t)(min(127, max(-128, q)) & 0xFF);
+}
+
+// Σq as the zero-point correction takes it, modulo 2^31: a block whose 1/d overflowed has
+// converted values of 0x80000000, and z·2^31 ≡ 0 (mod 2^32) for every even zero point z,
+// so IntegerGemm's −z·Σq + Σ u·q is unchanged. What is left lies within ±32·127.
+__device__ __forceinline__ int correction_sum(int sum)
+{
+    return (sum > 4096 || sum < -4096) ? (sum ^ (int)0x80000000) : sum;
+}
+
 __device__ __forceinline__ uint2 conversion_operand(int sum)
 {
+    sum = correction_sum(sum);
     const int hi = sum >> 6, lo = sum - 64 * hi;
     return make_uint2(half_bits(-6144) | (half_bits(-hi) << 16), half_bits(-lo));
 }
@@ -214,10 +238,10 @@ __device__ __forceinline__ QBlock quant_block8_values(float4 v, int semantics)
     int q0, q1, q2, q3;
     float dd;
     if (semantics == 0) {
-        q0 = (int)__builtin_rintf(v.x * inv);
-        q1 = (int)__builtin_rintf(v.y * inv);
-        q2 = (int)__builtin_rintf(v.z * inv);
-        q3 = (int)__builtin_rintf(v.w * inv);
+        q0 = cvt_rne_x86(v.x * inv);
+        q1 = cvt_rne_x86(v.y * inv);
+        q2 = cvt_rne_x86(v.z * inv);
+        q3 = cvt_rne_x86(v.w * inv);
         dd = d;
     } else {
         q0 = min(127, max(-127, (int)roundf(v.x * inv)));
@@ -230,8 +254,7 @@ __device__ __forceinline__ QBlock quant_block8_values(float4 v, int semantics)
     sum += dpp_i<DPP_XOR1>(sum);
     sum += dpp_i<DPP_XOR2>(sum);
     sum += dpp_i<DPP_HALF_MIRROR>(sum);
-    const uint32_t w = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-                       ((uint32_t)(q3 & 0xFF) << 24);
+    const uint32_t w = code_byte(q0) | (code_byte(q1) << 8) | (code_byte(q2) << 16) | (code_byte(q3) << 24);
     return QBlock{w, dd, sum};
 }
 
@@ -662,7 +685,7 @@ __device__ __forceinline__ void quant_block_pair(const float* y, int h, const Ac
     int sum = 0;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-        q[r] = (int)__builtin_rintf(y[r] * inv);
+        q[r] = cvt_rne_x86(y[r] * inv);
         sum += q[r];
     }
     sum += __shfl_xor(sum, 32);
@@ -670,8 +693,8 @@ __device__ __forceinline__ void quant_block_pair(const float* y, int h, const Ac
     int8_t* base = o.q + (((int64_t)(t >> 5) * o.B + b) * 2 * 32 + (t & 31)) * 16;
 #pragma unroll
     for (int g = 0; g < 4; g++) {
-        const uint32_t w = (uint32_t)(q[4 * g] & 0xFF) | ((uint32_t)(q[4 * g + 1] & 0xFF) << 8) |
-                           ((uint32_t)(q[4 * g + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * g + 3] & 0xFF) << 24);
+        const uint32_t w = code_byte(q[4 * g]) | (code_byte(q[4 * g + 1]) << 8) | (code_byte(q[4 * g + 2]) << 16) |
+                           (code_byte(q[4 * g + 3]) << 24);
         *reinterpret_cast<uint32_t*>(base + (g & 1) * 512 + 4 * h + 8 * (g >> 1)) = w;
     }
     if (h == 0) {
@@ -1445,7 +1468,7 @@ __global__ __launch_bounds__(256) void k_gemm_narrow(const uint8_t* __restrict__
                                  *reinterpret_cast<uint32_t*>(sAb + ((t * B + b) * 2 + hf) * 16 + idx) = qb.w;
                                  if (l8 == 0) {
                                      sDa[t * B + b] = qb.d;
-                                     sSum[t * B + b] = qb.sum;
+                                     sSum[t * B + b] = correction_sum(qb.sum);
                                      sDs[t * B + b] = qb.d * (float)qb.sum;
                                  }
                              },

@@ -139,11 +139,17 @@ def quantize_activations(x: np.ndarray, semantics: int = 0):
     return q, d, s
 
 
-def block_sums(qtype: int, w: np.ndarray, rows: int, cols: int, q: np.ndarray, tokens: int) -> np.ndarray:
+def block_sums(qtype: int, w: np.ndarray, rows: int, cols: int, q: np.ndarray, tokens: int,
+               s: np.ndarray | None = None) -> np.ndarray:
+    """s: the quantizer's int32 block sums; when omitted, the sums of the codes (the same
+    for every block whose codes did not saturate)."""
     w = _c(w, np.uint8)
     q = _c(q, np.int8)
+    if s is None:
+        s = q.reshape(tokens, cols // 32, 32).astype(np.int64).sum(axis=2)
+    s = _c(np.asarray(s).astype(np.int64).astype(np.int32), np.int32)
     out = np.empty((tokens, rows, cols // 32), np.int32)
-    if lib().ora_block_sums(qtype, _p(w), rows, cols, _p(q), None, tokens, _p(out)):
+    if lib().ora_block_sums(qtype, _p(w), rows, cols, _p(q), _p(s), tokens, _p(out)):
         raise ValueError("block_sums failed")
     return out
 

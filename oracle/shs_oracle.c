@@ -41,6 +41,7 @@
 #include "shs_oracle.h"
 
 #include <float.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <math.h>
 #include <stdlib.h>
@@ -321,6 +322,22 @@ int ora_quantize(int type, const float* src, uint8_t* dst, int64_t n)
 /* IntegerGemm.QuantizeActivations (IntegerGemm.cs:97-138): per 32 values
  * d = max|x|/127 (fp32, IEEE division), inv = d ≠ 0 ? 1/d : 0, q = RNE(x·inv)
  * (vcvtps2dq under the default rounding mode), s = Σq. */
+/* vcvtps2dq, which Avx.ConvertToVector256Int32 is: round to nearest even (the default
+ * MXCSR mode); NaN and anything outside the int32 range give 0x80000000. */
+static inline int32_t cvtps2dq(float v)
+{
+    float r = nearbyintf(v);
+    if (!(r >= -2147483648.0f && r < 2147483648.0f)) return INT32_MIN;
+    return (int32_t)r;
+}
+
+/* IntegerGemm.QuantizeActivations (IntegerGemm.cs:97-138): max|x| per block, d = max/127,
+ * inverse = 1/d (0 for an all-zero block), q = vcvtps2dq(x·inverse). The codes are the
+ * int32 values packed with signed saturation (vpackssdw, vpacksswb) to [-128, 127]; the
+ * block sum is the int32 sum of the unsaturated values, wrapping like Vector256<int> adds.
+ * |q| <= 127 for every finite block whose inverse is finite; a block max below 3.7e-37
+ * makes d so small that 1/d overflows to +inf, and then every value converts to
+ * 0x80000000 (code -128). */
 void ora_quantize_activations(const float* x, int64_t n, int8_t* q, float* d, int32_t* s)
 {
     for (int64_t b = 0; b < n / QK; b++) {
@@ -329,16 +346,24 @@ void ora_quantize_activations(const float* x, int64_t n, int8_t* q, float* d, in
         for (int j = 0; j < QK; j++) mx = fmaxf(mx, fabsf(xb[j]));
         float dd = mx / 127.0f;
         float inv = dd != 0.0f ? 1.0f / dd : 0.0f;
-        int32_t sum = 0;
+        uint32_t sum = 0;
         for (int j = 0; j < QK; j++) {
-            float v = xb[j] * inv;
-            int32_t qi = (int32_t)nearbyintf(v);
-            q[b * QK + j] = (int8_t)qi;
-            sum += qi;
+            int32_t qi = cvtps2dq(xb[j] * inv);
+            q[b * QK + j] = (int8_t)(qi < -128 ? -128 : qi > 127 ? 127 : qi);
+            sum += (uint32_t)qi;
         }
         d[b] = dd;
-        s[b] = sum;
+        s[b] = (int32_t)sum;
     }
+}
+
+/* (int)float as .NET 9+ converts on every platform: saturating, NaN to 0. */
+static inline int32_t dotnet_float_to_int(float v)
+{
+    if (v != v) return 0;
+    if (v >= 2147483648.0f) return INT32_MAX;
+    if (v <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)v;
 }
 
 /* IntegerDot.QuantizeActivations (IntegerDot.cs:60-98): same d and inverse, but the
@@ -354,7 +379,7 @@ void ora_quantize_activations_q8(const float* x, int64_t n, int8_t* q, float* d,
         int32_t sum = 0;
         for (int j = 0; j < QK; j++) {
             float v = xb[j] * inv;
-            int qi = (int)roundf(v); /* C roundf: half away from zero */
+            int qi = dotnet_float_to_int(roundf(v)); /* C roundf: half away from zero */
             if (qi < -127) qi = -127;
             if (qi > 127) qi = 127;
             q[b * QK + j] = (int8_t)qi;
@@ -421,18 +446,32 @@ static int unpack_row(int type, const uint8_t* row, int blocks, int8_t* w, float
 
 static int has_offset(int type) { return type == ORA_Q4_1 || type == ORA_Q5_1; }
 
-static inline int32_t block_dot(const int8_t* w, const int8_t* q)
+/* IntegerGemm.ZeroPoint (IntegerGemm.cs:75-81): the unsigned payload u = w + z. */
+static int zero_point(int type)
 {
-    int32_t acc = 0;
-    for (int k = 0; k < QK; k++) acc += (int32_t)w[k] * (int32_t)q[k];
-    return acc;
+    return type == ORA_Q4_0 ? 8 : type == ORA_Q5_0 ? 16 : type == ORA_Q8_0 ? 128 : 0;
+}
+
+/* The block sum as IntegerGemm forms it (IntegerGemm.cs:384-397): −z·Σa + Σ u·a in int32,
+ * with Σa the quantizer's block sum (sum) and a the saturated codes. u·a products and
+ * their sums are exact; the whole is taken modulo 2^32 like the vector adds. For every
+ * block whose codes did not saturate, Σa equals Σ codes and this is Σ (u − z)·a. */
+static inline int32_t block_dot(const int8_t* w, const int8_t* q, int z, int32_t sum)
+{
+    int32_t acc = 0, codes = 0;
+    for (int k = 0; k < QK; k++) {
+        acc += (int32_t)w[k] * (int32_t)q[k];
+        codes += q[k];
+    }
+    /* Σ u·a = Σ (w + z)·a = acc + z·Σ codes */
+    return (int32_t)((uint32_t)acc + (uint32_t)z * (uint32_t)codes - (uint32_t)z * (uint32_t)sum);
 }
 
 int ora_block_sums(int type, const uint8_t* w, int rows, int cols,
                    const int8_t* q, const int32_t* s, int tokens, int32_t* out)
 {
-    (void)s;
     if (cols % QK) return -1;
+    int z = zero_point(type);
     int blocks = cols / QK;
     int64_t rb = ora_row_bytes(type, cols);
     if (rb < 0) return -1;
@@ -444,7 +483,8 @@ int ora_block_sums(int type, const uint8_t* w, int rows, int cols,
         rc = unpack_row(type, w + (int64_t)r * rb, blocks, wr, sc, of);
         for (int t = 0; t < tokens; t++)
             for (int b = 0; b < blocks; b++)
-                out[((int64_t)t * rows + r) * blocks + b] = block_dot(wr + b * QK, q + (int64_t)t * cols + b * QK);
+                out[((int64_t)t * rows + r) * blocks + b] =
+                    block_dot(wr + b * QK, q + (int64_t)t * cols + b * QK, z, s[(int64_t)t * blocks + b]);
     }
     free(wr); free(sc); free(of);
     return rc;
@@ -462,7 +502,7 @@ int ora_matmul_q(int type, const uint8_t* w, int rows, int cols,
     int64_t rb = ora_row_bytes(type, cols);
     if (rb < 0) return -1;
     int out_rows = row_ids ? n_ids : rows;
-    int off = has_offset(type);
+    int off = has_offset(type), z = zero_point(type);
     int bad = 0;
     if (row_ids)
         for (int i = 0; i < n_ids; i++) if (row_ids[i] < 0 || row_ids[i] >= rows) bad = 1;
@@ -487,7 +527,7 @@ int ora_matmul_q(int type, const uint8_t* w, int rows, int cols,
                 const int32_t* st = s + (int64_t)t * blocks;
                 float acc = 0.0f;
                 for (int b = 0; b < blocks; b++) {
-                    int32_t I = block_dot(wr + b * QK, qt + b * QK);
+                    int32_t I = block_dot(wr + b * QK, qt + b * QK, z, st[b]);
                     float scale = sc[b] * dt[b];
                     acc = fmaf((float)I, scale, acc);
                     if (off) acc = fmaf(of[b], dt[b] * (float)st[b], acc);

@@ -32,12 +32,14 @@ def test_single_gemm_config_q4_0_9216x3072_t512_is_bit_exact(lib, oracle):
     assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("T", [128, 512])
 @pytest.mark.parametrize("qt", [2, 6, 7])
-def test_the_seven_projections_of_a_layer_are_bit_exact(lib, oracle, qt):
-    """q 3072→4096, k/v 3072→1024, o 4096→3072, gate/up 3072→9216, down 9216→3072."""
+def test_the_seven_projections_of_a_layer_are_bit_exact(lib, oracle, qt, T):
+    """q 3072→4096, k/v 3072→1024, o 4096→3072, gate/up 3072→9216, down 9216→3072, with
+    weights ~ N(0, 0.02) and activations ~ N(0, 1). T = 512 is the seven-projection
+    workload; the token count also selects the kernel's token-tile instantiation."""
     shapes = [(4096, 3072), (1024, 3072), (1024, 3072), (3072, 4096), (9216, 3072), (9216, 3072), (3072, 9216)]
-    rng = np.random.default_rng(qt)
-    T = 128
+    rng = np.random.default_rng(qt + T)
     for i, (rows, cols) in enumerate(shapes):
         w = _w(oracle, qt, rows, cols, seed=100 * qt + i)
         x = rng.standard_normal((T, cols)).astype(np.float32)
@@ -144,3 +146,91 @@ def test_device_pointer_entry_matches_host_entry(lib, oracle):
         hip.hipFree(xd)
         hip.hipFree(yd)
     assert np.array_equal(y, m.forward(x))
+
+
+def _same_bits_or_both_nan(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a)
+    return bool(np.array_equal(nan, np.isnan(b)) and np.array_equal(a[~nan].view(np.uint32), b[~nan].view(np.uint32)))
+
+
+def _edge_activations(T, cols, seed, with_saturating_blocks):
+    """N(0, 1) token rows with edge blocks planted at random (token, block) slots: all
+    zero; exact ties (max 127, so d = inv = 1 and ±2.5, 0.5, 1.5, 126.5 are ties); d
+    subnormal with a finite inverse (max 1e-36); very large maxima (1e30, 3e38); and, when
+    asked, the blocks whose values convert to 0x80000000 and saturate to code −128: maxima
+    whose 1/d overflows (1e-37, 1e-40) and one infinite element."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, cols)).astype(np.float32)
+    tie = np.zeros(32, np.float32)
+    tie[:8] = [127.0, 2.5, -2.5, 3.5, 0.5, -0.5, 1.5, -126.5]
+    kinds = ["zero", "tie", 1e-36, 1e30, 3e38] + (["inf", 1e-37, 1e-40] if with_saturating_blocks else [])
+    B = cols // 32
+    for n, kind in enumerate(kinds * 6):
+        t, b = int(rng.integers(T)), int(rng.integers(B))
+        blk = x[t, 32 * b:32 * b + 32]
+        if kind == "zero":
+            blk[:] = 0
+        elif kind == "tie":
+            blk[:] = rng.permutation(tie) * (1 if n % 2 else -1)
+        elif kind == "inf":
+            blk[int(rng.integers(32))] = np.inf * (1 if n % 2 else -1)
+        else:
+            blk[:] = (blk / np.abs(blk).max() * kind).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("qt", TYPES)
+@pytest.mark.parametrize("semantics", [0, 1])
+def test_activation_edge_blocks_are_bit_exact(lib, oracle, qt, semantics):
+    """The quantizer's edges (IntegerDotTests.cs:128-173, IntegerGemm.cs:89-95) through the
+    whole GEMM at 100 rows × 3072 × 45 tokens (partial row and token tiles), and through
+    the decode-width kernel for the first 4 tokens. Outputs that overflow to ±inf or NaN
+    (an infinite element, or a 3e38 max times a weight scale) are compared as NaN = NaN
+    (the NaN payload is the hardware's). For Q8_0 the saturating blocks are left out: its
+    kernel multiplies the signed bytes, so its zero-point correction comes from the
+    saturated codes, where IntegerGemm's comes from the wrapped int32 block sum (a known
+    divergence, only for blocks holding a non-finite value or a max below 3.7e-37)."""
+    rows, cols, T = 100, 3072, 45
+    w = H.random_blocks(qt, rows, cols, seed=70 + qt)
+    x = _edge_activations(T, cols, seed=qt + 10 * semantics, with_saturating_blocks=qt != 8)
+    m = lib.WeightMatrix(qt, rows, cols, w)
+    with np.errstate(all="ignore"):
+        ref = oracle.matmul(qt, w, rows, cols, x, T, semantics=semantics)
+    y = m.forward(x, semantics=semantics)
+    assert _same_bits_or_both_nan(y, ref)
+    if semantics == 0:
+        assert _same_bits_or_both_nan(m.forward(x[:4]), ref[:4])
+        assert _same_bits_or_both_nan(m.forward(x[3:4]), ref[3:4])
+
+
+@pytest.mark.parametrize("qt", [2, 3, 6, 7])
+def test_block_sums_at_the_activation_edges(lib, oracle, qt):
+    """The exact int32 block sums −z·Σa + Σ u·a for the edge blocks, against the oracle fed
+    the quantizer's own block sums (wrapped, as IntegerGemm's int32 vector adds wrap)."""
+    rows, cols, T = 64, 1024, 33
+    w = H.random_blocks(qt, rows, cols, seed=90 + qt)
+    x = _edge_activations(T, cols, seed=5, with_saturating_blocks=True)
+    with np.errstate(all="ignore"):
+        q, d, s = oracle.quantize_activations(x)
+    got = lib.WeightMatrix(qt, rows, cols, w).block_sums(x)
+    assert np.array_equal(got, oracle.block_sums(qt, w, rows, cols, q, T, s))
+
+
+@pytest.mark.parametrize("qt", [6, 7])
+def test_q5_blocks_with_every_fifth_bit_set_at_t512(lib, oracle, qt):
+    """Q5_0/Q5_1 weights whose 32 high bits are all set (u = 16..31), mixed with random
+    blocks, at 512 tokens, 100 rows (a partial row tile) and 500 tokens (a partial token tile)."""
+    rows, cols = 100, 3072
+    w = H.random_blocks(qt, rows, cols, seed=qt).reshape(-1, H.TYPE_SIZE[qt]).copy()
+    qh = 2 if qt == 6 else 4
+    rng = np.random.default_rng(qt)
+    pick = rng.random(w.shape[0]) < 0.5
+    w[pick, qh:qh + 4] = 0xFF
+    w = w.reshape(-1)
+    m = lib.WeightMatrix(qt, rows, cols, w)
+    for T in (512, 500):
+        x = rng.standard_normal((T, cols)).astype(np.float32)
+        y = m.forward(x)
+        ref = oracle.matmul(qt, w, rows, cols, x, T)
+        assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), T

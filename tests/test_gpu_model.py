@@ -373,3 +373,68 @@ def test_device_exp_is_the_oracle_exp_bit_for_bit(shs, oracle):
     lib = oracle.lib()
     ref = np.array([lib.ora_expf(float(v)) for v in x], np.float32)
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+YARN = dict(rope_scale=16.0, rope_orig_ctx=16, yarn_active=1, yarn_beta_fast=32.0, yarn_beta_slow=1.0,
+            yarn_ext_factor=1.0, yarn_mscale=1.0, yarn_mscale_all_dim=1.0, attn_temperature=0.1)
+
+
+def test_the_real_checkpoints_rope_keys_run_yarn_and_the_query_temperature(shs, oracle, tmp_path):
+    """A GGUF carrying the converter's YaRN and temperature keys
+    (tools/convert_shieldstral_to_gguf.py:307-323), opened through shs_open: YarnActive
+    (ModelConfig.cs:54-56), the YaRN frequencies (Rope.cs:33-106) and, with a 16-token
+    original context, the Llama-4 query temperature from position 16 on
+    (MinistralModel.cs:471-482). A 40-token prefill (every capture), then 1-, 2- and
+    4-token steps and the KV cache, bit-exact against the oracle."""
+    import gguf_writer as GW
+    cfg = oracle.make_config(n_layer=2, hidden=256, n_head=8, n_kv_head=2, head_dim=128, ffn=512, vocab=512, **YARN)
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=61)
+    path = tmp_path / "yarn.gguf"
+    GW.write_gguf(path, "mistral3", cfg, tensors, types, extra_kv=GW.yarn_keys("mistral3", cfg))
+    gpu = shs.MinistralModel.open(str(path), initial_cache_capacity=64)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=64)
+    try:
+        c = gpu.config
+        assert c.yarn_active and c.rope_original_context_length == 16 and c.attention_temperature_scale > 0
+        toks = np.random.default_rng(8).integers(0, cfg.vocab, 47)
+        gcap, ocap = {}, {}
+        gpu.set_capture(lambda n, a: gcap.__setitem__(n, a))
+        try:
+            g = gpu.forward(toks[:40])
+        finally:
+            gpu.set_capture(None)
+        o = ora.forward(toks[:40], head_mode=2, capture=lambda n, a: ocap.__setitem__(n, a))
+        assert set(gcap) == set(ocap)
+        for name in sorted(gcap):
+            assert np.array_equal(gcap[name], ocap[name]), name
+        assert np.array_equal(g, o)
+        for a, b in ((40, 41), (41, 43), (43, 47)):
+            g = gpu.forward(toks[a:b])
+            o = ora.forward(toks[a:b], head_mode=2)
+            assert np.array_equal(g.view(np.uint32), o.view(np.uint32)), (a, b)
+        assert np.array_equal(gpu.kv_cache.snapshot(47), ora.snapshot(47))
+    finally:
+        gpu.close()
+
+
+def test_decode_at_the_full_layer_width_matches_the_oracle(shs, oracle):
+    """The decode-width kernels at the real layer shape (hidden 3072, FFN 9216, 32 query and
+    8 KV heads; two layers, 4096-entry vocabulary): the q|k|v and gate|up kernels that
+    normalize their own input row (96 blocks: the 16-step register rounds iterate), the
+    fused RoPE/KV-store and SwiGLU epilogues and the decode attention with 8 KV heads. A
+    40-token prefill, then 1-, 2- and 4-token steps: full logits and the KV cache bit-exact."""
+    cfg = oracle.make_config(n_layer=2, hidden=3072, n_head=32, n_kv_head=8, head_dim=128, ffn=9216, vocab=4096)
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=62)
+    gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types,
+                                          initial_cache_capacity=64)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=64)
+    try:
+        toks = np.random.default_rng(9).integers(0, cfg.vocab, 47)
+        assert np.array_equal(gpu.forward(toks[:40]), ora.forward(toks[:40], head_mode=2))
+        for a, b in ((40, 41), (41, 42), (42, 44), (44, 47)):
+            g = gpu.forward(toks[a:b])
+            o = ora.forward(toks[a:b], head_mode=2)
+            assert np.array_equal(g.view(np.uint32), o.view(np.uint32)), (a, b, H.rel_l2(g, o))
+            assert np.array_equal(gpu.kv_cache.snapshot(b), ora.snapshot(b)), (a, b)
+    finally:
+        gpu.close()

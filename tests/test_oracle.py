@@ -139,6 +139,82 @@ def test_activation_quantization_matches_numpy_float32(oracle):
     assert np.array_equal(s.reshape(16, -1), sn)
 
 
+def edge_blocks():
+    """Activation blocks at the quantizer's edges, one per 32-value block: all zero; exact
+    ties; a max that makes d subnormal with a finite inverse (1e-36); a max whose d is so
+    small that 1/d overflows to +inf (1e-37 and 1e-40); very large maxima (1e30, 3e38);
+    one infinite element; ordinary N(0, 1)."""
+    rng = np.random.default_rng(77)
+    blocks = [np.zeros(32)]
+    tie = np.zeros(32)
+    tie[:8] = [127.0, 2.5, -2.5, 3.5, 0.5, -0.5, 1.5, -126.5]
+    blocks.append(tie)
+    for mx in (1e-36, 1e-37, 1e-40, 1e30, 3e38):
+        b = rng.standard_normal(32)
+        blocks.append(b / np.abs(b).max() * mx)
+    inf = rng.standard_normal(32)
+    inf[5] = np.inf
+    blocks.append(inf)
+    blocks.append(rng.standard_normal(32))
+    return np.concatenate(blocks).astype(np.float32)
+
+
+def test_activation_quantization_at_the_edges_follows_the_x86_conversion(oracle):
+    """IntegerGemm.QuantizeActivations converts with vcvtps2dq, packs with signed
+    saturation and sums the unsaturated int32 values (IntegerGemm.cs:110-136). numpy's
+    float32 → int32 cast on this x86 host is the same conversion (NaN and out-of-range
+    give 0x80000000), so it restates the edges independently: a block whose 1/d
+    overflows converts every value to 0x80000000 (code −128, sum 32·2^31 ≡ 0 mod 2^32),
+    and an infinite element makes d infinite, inverse 0 and that value NaN."""
+    x = edge_blocks()
+    q, d, s = oracle.quantize_activations(x, 0)
+    xb = x.reshape(-1, 32)
+    mx = np.max(np.abs(xb), axis=1)
+    dn = (mx / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        inv = np.where(dn != 0, np.float32(1) / dn, np.float32(0)).astype(np.float32)
+        v = np.rint((xb * inv[:, None]).astype(np.float32))
+        q32 = v.astype(np.int32)
+    assert np.array_equal(d, dn)
+    assert np.array_equal(q.reshape(-1, 32), np.clip(q32, -128, 127).astype(np.int8))
+    assert np.array_equal(s, (q32.astype(np.int64).sum(axis=1) % 2 ** 32).astype(np.uint32).view(np.int32))
+    assert np.isinf(inv[3]) and np.all(q32[3] == np.iinfo(np.int32).min) and s[3] == 0
+    assert list(q[32:40]) == [127, 2, -2, 4, 0, 0, 2, -126]
+    assert 0 < d[2] < np.finfo(np.float32).tiny and np.isfinite(inv[2]) and np.abs(q32[2]).max() == 127
+    assert q32[7, 5] == np.iinfo(np.int32).min and s[7] == np.iinfo(np.int32).min
+
+
+def test_dot_semantics_at_the_edges(oracle):
+    """IntegerDot rounds half away from zero, converts as .NET 9+ does (saturating, NaN to
+    0) and clamps to ±127; its scale is stored as fp16, so a block max below ≈3.8e-6 keeps
+    d = 0 while its codes still come from the float inverse."""
+    x = edge_blocks()
+    q, d, s = oracle.quantize_activations(x, 1)
+    assert list(q[32:40]) == [127, 3, -3, 4, 1, -1, 2, -127]
+    assert np.all(q.reshape(-1, 32)[3] == np.where(x.reshape(-1, 32)[3] > 0, 127, -127))
+    assert d[2] == 0 and d[3] == 0 and q.reshape(-1, 32)[7, 5] == 0
+    assert np.array_equal(s, q.reshape(-1, 32).astype(np.int64).sum(axis=1))
+
+
+def test_block_sums_follow_the_zero_point_form_at_the_edges(oracle):
+    """I = −z·Σa + Σ u·a in int32 (IntegerGemm.cs:384-397), from the quantizer's block sum,
+    brute-forced in int64 and wrapped; for the saturated blocks this differs from
+    Σ (u − z)·codes."""
+    x = edge_blocks()
+    q, d, s = oracle.quantize_activations(x, 0)
+    T, cols = 1, x.size
+    for qt in (2, 3, 6, 7, 8):
+        w = H.random_blocks(qt, 3, cols, seed=qt)
+        got = oracle.block_sums(qt, w, 3, cols, q, T, s)
+        wi, _, _ = NR.decode_blocks(qt, w, 3, cols)
+        z = {2: 8, 3: 0, 6: 16, 7: 0, 8: 128}[qt]
+        u = wi.reshape(3, -1, 32) + z
+        qq = q.reshape(-1, 32).astype(np.int64)
+        ref = np.einsum("rbk,bk->rb", u, qq) - z * s.astype(np.int64)[None, :]
+        ref = (ref % 2 ** 32).astype(np.uint32).view(np.int32)
+        assert np.array_equal(got[0], ref), qt
+
+
 def test_dot_semantics_scale_is_fp16_rounded(oracle):
     x = np.random.default_rng(4).standard_normal(3072).astype(np.float32)
     _, d0, _ = oracle.quantize_activations(x, 0)
