@@ -17,6 +17,7 @@
 #include <map>
 #include <string>
 #include <vector>
+#include <ctime>
 
 using namespace shs;
 
@@ -384,6 +385,10 @@ struct shs_model {
     void* cap_user = nullptr;
     Profiler prof;
     std::map<std::string, TensorLoc> where;
+    // One completion event per layer, recorded when a pass can be cancelled (created on
+    // first use): the host keeps at most CANCEL_LOOKAHEAD layers queued ahead of the GPU
+    // and polls the flag while it waits for the oldest of them.
+    std::vector<hipEvent_t> layer_done;
 };
 
 // ------------------------------------------------------------------ RoPE
@@ -626,6 +631,7 @@ void destroy_model(shs_model* m)
     }
     if (m->kc) (void)hipFree(m->kc);
     if (m->vc) (void)hipFree(m->vc);
+    for (hipEvent_t e : m->layer_done) (void)hipEventDestroy(e);
     hipStream_t s = m->stream;
     delete m;
     if (s) (void)hipStreamDestroy(s);
@@ -958,9 +964,43 @@ shs_status ensure_work(shs_model* m, int T)
     return SHS_OK;
 }
 
+// Layers a cancellable pass queues ahead of the one the GPU is running: enough to keep
+// the GPU fed between the host's polls, few enough that a cancel is seen within about
+// two layers of execution (ModerationCancellationTests.cs:50-74).
+constexpr int CANCEL_LOOKAHEAD = 2;
+
+// Before layer l of a cancellable pass is queued: waits until layer l − CANCEL_LOOKAHEAD
+// has run on the GPU, polling the flag meanwhile. Returns SHS_E_CANCELLED (after the
+// queued layers drain) once the flag is set.
+shs_status cancel_point(shs_model* m, int l, int l_begin, const volatile int32_t* cancel)
+{
+    auto cancelled = [&] {
+        (void)hipStreamSynchronize(m->stream);
+        return fail(SHS_E_CANCELLED, "The operation was canceled.");
+    };
+    if (*cancel) return cancelled();
+    if (m->layer_done.empty()) {
+        m->layer_done.assign(m->cfg.n_layer, nullptr);
+        for (auto& e : m->layer_done) HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    const int wait_for = l - CANCEL_LOOKAHEAD;
+    if (wait_for < l_begin) return SHS_OK;
+    for (;;) {
+        const hipError_t q = hipEventQuery(m->layer_done[wait_for]);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) return hip_fail(q, "hipEventQuery");
+        if (*cancel) return cancelled();
+        struct timespec ts = {0, 20000};  // 20 µs between polls
+        nanosleep(&ts, nullptr);
+    }
+    return *cancel ? cancelled() : SHS_OK;
+}
+
 // The decoder layers over the T tokens in m->h. Keys and values for token t go to cache
 // slot slot0 + t of (kc, vc) whose per-head stride is cap positions; attention runs over
-// the given work items. cancel is polled between layers.
+// the given work items. With a cancel flag, at most CANCEL_LOOKAHEAD layers are queued
+// ahead of the GPU and the flag is polled while the host waits for them, so a cancel
+// set during execution is observed between layers.
 shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap, int slot0, int l_begin, int l_end,
                       const AttnItem* items_dev, int n_items, const volatile int32_t* cancel, bool per_layer_kv)
 {
@@ -981,9 +1021,9 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
     HIP_TRY(m->act.ensure(T, std::max(std::max(hidden, qdim), c.ffn), &a));
 
     for (int l = l_begin; l < l_end; l++) {
-        if (cancel && *cancel) {
-            (void)hipStreamSynchronize(m->stream);
-            return fail(SHS_E_CANCELLED, "The operation was canceled.");
+        if (cancel) {
+            shs_status cs = cancel_point(m, l, l_begin, cancel);
+            if (cs != SHS_OK) return cs;
         }
         const Layer& L = m->layers[l];
         float* kc = per_layer_kv ? kc_all + kv_layer_floats(m, cap) * l : kc_all;
@@ -1139,6 +1179,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         } else {
             if (run_proj(m, L.down, af, h, hidden, GEMM_ADD, "gemm_down") != SHS_OK) return SHS_E_DEVICE;
         }
+        if (cancel) HIP_TRY(hipEventRecord(m->layer_done[l], m->stream));
     }
     return SHS_OK;
 }

@@ -552,7 +552,10 @@ def device_expf(x, device: int = 0) -> np.ndarray:
 
 
 class CancellationFlag:
-    """A host int the library polls between layer launches (the CancellationToken)."""
+    """A host int the library polls between layers while they run (the CancellationToken):
+    a cancellable pass keeps at most two layers queued ahead of the GPU and checks the
+    flag while it waits for them, so a cancel set from another thread mid-pass is seen
+    within about two layers."""
 
     def __init__(self):
         self._v = C.c_int32(0)

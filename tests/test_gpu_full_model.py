@@ -108,3 +108,37 @@ def test_ragged_q5_1_batch_longest_and_shortest_prompts_match_the_oracle(shs, or
             assert np.array_equal(batch[s].view(np.uint32), ref.view(np.uint32)), (s, int(lens[s]))
     finally:
         m.close()
+
+
+def test_a_cancel_from_another_thread_stops_a_running_verdict(shs, full_q4):
+    """ModerationCancellationTests.cs:50-74 on the full model: a thread sets the flag a few
+    milliseconds into a 1024-token pass (about 14 ms of GPU work). The pass raises
+    OperationCanceledError, the KV length stays at the prefilled 100 tokens, and the
+    next verdict is bit-identical to an uncancelled one. Thread timing is not exact, so
+    several delays are tried and at least one must land mid-pass."""
+    import threading
+    import time
+    m = full_q4
+    rng = np.random.default_rng(77)
+    toks = rng.integers(0, 131072, 1124)
+    ids = [11, 12]
+    m.reset_kv_cache()
+    m.prefill(toks[:100])
+    expected = m.forward_selected(toks[100:], ids)
+    cancelled = 0
+    for delay_ms in (2.0, 4.0, 6.0):
+        m.reset_kv_cache()
+        m.prefill(toks[:100])
+        flag = shs.CancellationFlag()
+        t = threading.Thread(target=lambda: (time.sleep(delay_ms / 1e3), flag.cancel()))
+        t.start()
+        try:
+            got = m.forward_selected(toks[100:], ids, cancel=flag)
+            assert np.array_equal(got, expected)  # finished before the flag was set
+            assert m.cached_token_count == 1124
+        except shs.OperationCanceledError:
+            cancelled += 1
+            assert m.cached_token_count == 100
+            assert np.array_equal(m.forward_selected(toks[100:], ids), expected)
+        t.join()
+    assert cancelled >= 1

@@ -438,3 +438,33 @@ def test_decode_at_the_full_layer_width_matches_the_oracle(shs, oracle):
             assert np.array_equal(gpu.kv_cache.snapshot(b), ora.snapshot(b)), (a, b)
     finally:
         gpu.close()
+
+
+def test_a_cancel_set_while_the_layers_run_is_observed(shs, tiny):
+    """ModerationCancellationTests.cs:50-74: the flag is set after layer 0 has run on the
+    GPU (from the activation callback, so the moment is exact), and the pass stops before
+    layer 1 with OperationCanceledError; the KV length does not move and the next request
+    scores exactly like a fresh one."""
+    cfg, tensors, types, gpu, ora = tiny
+    toks = np.random.default_rng(13).integers(0, cfg.vocab, 60)
+    gpu.reset_kv_cache()
+    expected = gpu.forward_selected(toks, [4, 9])
+    gpu.reset_kv_cache()
+    gpu.prefill(toks[:12])
+    flag = shs.CancellationFlag()
+    seen = []
+
+    def sink(name, arr):
+        seen.append(name)
+        if name == "blk.0.output":
+            flag.cancel()
+
+    gpu.set_capture(sink)
+    try:
+        with pytest.raises(shs.OperationCanceledError):
+            gpu.forward_selected(toks[12:], [4, 9], cancel=flag)
+    finally:
+        gpu.set_capture(None)
+    assert "blk.0.output" in seen and not any(n.startswith("blk.1.") for n in seen)
+    assert gpu.cached_token_count == 12
+    assert np.array_equal(gpu.forward_selected(toks[12:], [4, 9]), expected)
