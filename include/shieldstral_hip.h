@@ -175,6 +175,16 @@ shs_status shs_matmul_block_sums(shs_matrix* m, const float* x, int32_t tokens, 
  * stream and returns when the result is written. */
 shs_status shs_matmul_device(shs_matrix* m, const float* x_dev, int32_t tokens, float* y_dev);
 
+/* No counterpart in the reference: shs_matmul_device for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and bit-identical results; the activation codes go to a fixed
+ * 16 MiB scratch array per GPU that the library holds until the process ends, so no
+ * hipMalloc, hipFree or allocating call runs. tokens·(cols + cols/2) bytes, rounded up,
+ * must fit in it (SHS_E_OUT_OF_RANGE otherwise: about 3600 tokens at 3072 columns).
+ * Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (from
+ * several threads or matrices) race and must be serialised by the caller. */
+shs_status shs_matmul_device_noalloc(shs_matrix* m, const float* x_dev, int32_t tokens, float* y_dev);
+
 /* e^x as the attention softmax and SwiGLU's sigmoid evaluate it on the device, for
  * x[0..n) → y (host buffers). Parity instrumentation: the CPU restatement performs the
  * same sequence of IEEE operations, and this entry lets a test compare them directly. */

@@ -1637,6 +1637,43 @@ extern "C" shs_status shs_matmul_device(shs_matrix* m, const float* x_dev, int32
     return SHS_OK;
 }
 
+// shs_matmul_device with the activation codes in the library's fixed per-GPU scratch
+// (noalloc_scratch): no hipMalloc, hipFree or allocating library call on any path.
+extern "C" shs_status shs_matmul_device_noalloc(shs_matrix* m, const float* x_dev, int32_t T, float* y_dev)
+{
+    if (!m || !x_dev || !y_dev) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
+    if (T <= 0) return fail(SHS_E_INVALID_ARGUMENT, "tokens must be positive");
+    const int K = m->w.cols, B = K / 32;
+    const size_t Tpad = ((size_t)T + 31) / 32 * 32;
+    auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const size_t q_bytes = up(Tpad * (size_t)K), f_bytes = up(sizeof(float) * Tpad * B),
+                 cv_bytes = up(sizeof(uint2) * Tpad * B);
+    const size_t need = q_bytes + cv_bytes + 2 * f_bytes;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(SHS_E_OUT_OF_RANGE,
+                    "%d tokens of %d columns need %zu bytes of activation scratch; shs_matmul_device_noalloc holds "
+                    "at most %zu (about %zu tokens at this width). Split the call or use shs_matmul_device.",
+                    T, K, need, NOALLOC_SCRATCH_BYTES, NOALLOC_SCRATCH_BYTES / ((size_t)K + 16 * (size_t)B));
+    HIP_TRY(hipSetDevice(m->device));
+    uint8_t* base = nullptr;
+    HIP_TRY(noalloc_scratch(m->device, &base));
+    ActQ8 a;
+    a.T = T;
+    a.Tpad = (int)Tpad;
+    a.K = K;
+    a.B = B;
+    a.q = reinterpret_cast<int8_t*>(base);
+    a.d = reinterpret_cast<float*>(base + q_bytes);
+    a.ds = reinterpret_cast<float*>(base + q_bytes + f_bytes);
+    a.cv = reinterpret_cast<uint2*>(base + q_bytes + 2 * f_bytes);
+    // k_quant_act writes every code, scale and column up to Tpad (zeros past T), so nothing
+    // left by an earlier call is read.
+    HIP_TRY(launch_quant_act(x_dev, K, a, 0, m->stream));
+    HIP_TRY(launch_gemm(m->w, a, y_dev, m->w.rows, GEMM_STORE, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return SHS_OK;
+}
+
 // Error hook for the GGUF reader (shs_gguf.cpp), which shares this thread-local message.
 extern "C" __attribute__((visibility("hidden"))) shs_status shs_gguf_fail(shs_status code, const char* msg)
 {

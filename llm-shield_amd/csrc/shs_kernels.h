@@ -172,4 +172,11 @@ hipError_t launch_synth_f32(uint64_t seed, uint64_t tensor_id, int64_t n, float 
 // Inverse of launch_repack: rows [0, rows) back to native GGUF blocks.
 hipError_t launch_unpack_native(const DevMatrix& m, int row0, int nrows, uint8_t* native, hipStream_t s);
 
+// Fixed device scratch for callers that cannot allocate: one array of this many bytes per
+// GPU, in the code object, held until the process ends. noalloc_scratch() returns the
+// array's device address on `device` (looked up once per device with that device made
+// current, then cached); host code uses only that address, never the array's name.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(16) << 20;
+hipError_t noalloc_scratch(int device, uint8_t** out);
+
 }  // namespace shs

@@ -6,6 +6,7 @@
 // 376-418), RMSNorm's accumulation order (Kernels.cs:26-61) and RoPE's rotation
 // (Rope.cs:112-135). The file is compiled with -ffp-contract=off; every fma is explicit.
 #include "shs_kernels.h"
+#include <mutex>
 #include <type_traits>
 
 #include <math.h>
@@ -3207,6 +3208,29 @@ hipError_t launch_unpack_native(const DevMatrix& w, int row0, int nrows, uint8_t
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+// ------------------------------------------------- fixed scratch (no allocation)
+
+// The activation codes of shs_matmul_device_noalloc. Its host-side name is a stand-in, not
+// a device address: kernels get the address noalloc_scratch() looks up.
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+hipError_t noalloc_scratch(int device, uint8_t** out)
+{
+    static std::mutex mu;
+    static uint8_t* addr[64] = {};
+    if (device < 0 || device >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[device]) {
+        hipError_t e = hipSetDevice(device);
+        if (e != hipSuccess) return e;
+        void* p = nullptr;
+        if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+        addr[device] = static_cast<uint8_t*>(p);
+    }
+    *out = addr[device];
+    return hipSuccess;
 }
 
 }  // namespace shs

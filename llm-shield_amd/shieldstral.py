@@ -104,6 +104,7 @@ EXPORTS = (
     "shs_get_config", "shs_kv_reset", "shs_kv_length", "shs_kv_capacity", "shs_kv_snapshot", "shs_kv_restore",
     "shs_forward", "shs_forward_batch", "shs_set_capture", "shs_layer_forward", "shs_matrix_create",
     "shs_matrix_free", "shs_matmul", "shs_matmul_rows", "shs_matmul_block_sums", "shs_matmul_device",
+    "shs_matmul_device_noalloc",
     "shs_profile_enable", "shs_profile_read", "shs_profile_reset", "shs_synchronize",
     "shs_debug_expf",
 )
@@ -152,6 +153,7 @@ def _declare(L: C.CDLL) -> None:
         "shs_matmul_rows": [P, P, I32, P, I32, P],
         "shs_matmul_block_sums": [P, P, I32, P],
         "shs_matmul_device": [P, P, I32, P],
+        "shs_matmul_device_noalloc": [P, P, I32, P],
         "shs_profile_enable": [P, I32],
         "shs_profile_read": [P, C.c_char_p, C.POINTER(I64), C.POINTER(C.c_double), C.POINTER(C.c_double)],
         "shs_profile_reset": [P],
@@ -315,6 +317,11 @@ class WeightMatrix:
     def forward_device(self, x_ptr: int, tokens: int, y_ptr: int) -> None:
         """y_dev = x_dev·Wᵀ for activations already in HBM (device pointers)."""
         _check(_lib.shs_matmul_device(self._h, C.c_void_p(x_ptr), tokens, C.c_void_p(y_ptr)))
+
+    def forward_device_noalloc(self, x_ptr: int, tokens: int, y_ptr: int) -> None:
+        """forward_device with the activation codes in the library's fixed per-GPU scratch:
+        allocates nothing. Calls that overlap on one GPU race on that scratch."""
+        _check(_lib.shs_matmul_device_noalloc(self._h, C.c_void_p(x_ptr), tokens, C.c_void_p(y_ptr)))
 
 
 # ------------------------------------------------------------------ model
