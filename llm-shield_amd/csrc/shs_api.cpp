@@ -98,24 +98,12 @@ struct HostBuf {
 };
 
 struct ActBuf {
-    Buf q, d, cv, ds;
+    Buf all;  // act_q8_view's layout
     hipError_t ensure(int T, int K, ActQ8* view)
     {
-        int Tpad = (T + 31) / 32 * 32;
-        int B = K / 32;
-        hipError_t e;
-        if ((e = q.ensure((size_t)Tpad * K)) != hipSuccess) return e;
-        if ((e = d.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
-        if ((e = cv.ensure(sizeof(uint2) * (size_t)Tpad * B)) != hipSuccess) return e;
-        if ((e = ds.ensure(sizeof(float) * (size_t)Tpad * B)) != hipSuccess) return e;
-        view->T = T;
-        view->Tpad = Tpad;
-        view->K = K;
-        view->B = B;
-        view->q = q.as<int8_t>();
-        view->d = d.as<float>();
-        view->cv = cv.as<uint2>();
-        view->ds = ds.as<float>();
+        hipError_t e = all.ensure(act_q8_bytes(T, K));
+        if (e != hipSuccess) return e;
+        *view = act_q8_view(all.p, T, K);
         return hipSuccess;
     }
 };
@@ -1643,29 +1631,17 @@ extern "C" shs_status shs_matmul_device_noalloc(shs_matrix* m, const float* x_de
 {
     if (!m || !x_dev || !y_dev) return fail(SHS_E_INVALID_ARGUMENT, "null argument");
     if (T <= 0) return fail(SHS_E_INVALID_ARGUMENT, "tokens must be positive");
-    const int K = m->w.cols, B = K / 32;
-    const size_t Tpad = ((size_t)T + 31) / 32 * 32;
-    auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    const size_t q_bytes = up(Tpad * (size_t)K), f_bytes = up(sizeof(float) * Tpad * B),
-                 cv_bytes = up(sizeof(uint2) * Tpad * B);
-    const size_t need = q_bytes + cv_bytes + 2 * f_bytes;
+    const int K = m->w.cols;
+    const size_t need = act_q8_bytes(T, K);
     if (need > NOALLOC_SCRATCH_BYTES)
         return fail(SHS_E_OUT_OF_RANGE,
                     "%d tokens of %d columns need %zu bytes of activation scratch; shs_matmul_device_noalloc holds "
                     "at most %zu (about %zu tokens at this width). Split the call or use shs_matmul_device.",
-                    T, K, need, NOALLOC_SCRATCH_BYTES, NOALLOC_SCRATCH_BYTES / ((size_t)K + 16 * (size_t)B));
+                    T, K, need, NOALLOC_SCRATCH_BYTES, NOALLOC_SCRATCH_BYTES / ((size_t)K + (size_t)K / 2));
     HIP_TRY(hipSetDevice(m->device));
     uint8_t* base = nullptr;
     HIP_TRY(noalloc_scratch(m->device, &base));
-    ActQ8 a;
-    a.T = T;
-    a.Tpad = (int)Tpad;
-    a.K = K;
-    a.B = B;
-    a.q = reinterpret_cast<int8_t*>(base);
-    a.d = reinterpret_cast<float*>(base + q_bytes);
-    a.ds = reinterpret_cast<float*>(base + q_bytes + f_bytes);
-    a.cv = reinterpret_cast<uint2*>(base + q_bytes + 2 * f_bytes);
+    ActQ8 a = act_q8_view(base, T, K);
     // k_quant_act writes every code, scale and column up to Tpad (zeros past T), so nothing
     // left by an earlier call is read.
     HIP_TRY(launch_quant_act(x_dev, K, a, 0, m->stream));

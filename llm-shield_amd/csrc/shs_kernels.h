@@ -43,6 +43,31 @@ struct ActQ8 {
     float* ds = nullptr;
 };
 
+// The four arrays of an ActQ8 live in one allocation, in this order, each 256-byte
+// aligned: codes [Tpad·K], d_a and d_a·Σq [Tpad·B] fp32, conversion columns [Tpad·B]. The
+// GEMM addresses all of them from the codes' base with 32-bit offsets.
+inline size_t act_q8_round(size_t v) { return (v + 255) & ~(size_t)255; }
+inline size_t act_q8_bytes(int T, int K)
+{
+    const size_t Tpad = ((size_t)T + 31) / 32 * 32, B = (size_t)K / 32;
+    return act_q8_round(Tpad * K) + 2 * act_q8_round(4 * Tpad * B) + act_q8_round(8 * Tpad * B);
+}
+inline ActQ8 act_q8_view(void* base, int T, int K)
+{
+    ActQ8 a;
+    a.T = T;
+    a.Tpad = (T + 31) / 32 * 32;
+    a.K = K;
+    a.B = K / 32;
+    const size_t qb = act_q8_round((size_t)a.Tpad * K), fb = act_q8_round(4 * (size_t)a.Tpad * a.B);
+    uint8_t* p = static_cast<uint8_t*>(base);
+    a.q = reinterpret_cast<int8_t*>(p);
+    a.d = reinterpret_cast<float*>(p + qb);
+    a.ds = reinterpret_cast<float*>(p + qb + fb);
+    a.cv = reinterpret_cast<uint2*>(p + qb + 2 * fb);
+    return a;
+}
+
 // One attention work item: q_count ≤ 32 queries of one sequence at rows q_start.. of q/ctx,
 // the first at position pos0, attending to cache indices key_start .. key_start + pos0 +
 // q_count − 1 (query i sees pos0 + i + 1 keys). Scores of the item's heads go to scratch + s_off.

@@ -608,6 +608,28 @@ __device__ __forceinline__ void lds_copy4(const void* g, uint32_t lds)
 {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
+// The same copies addressed as a scalar base plus a per-lane 32-bit offset (the saddr
+// form): no vector instruction forms the address. The masked form copies only the lanes of
+// `mask` (exec is saved and restored inside the one asm statement).
+__device__ __forceinline__ void lds_copy16_s(const void* sbase, uint32_t voff, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy16_s_masked(const void* sbase, uint32_t voff, uint32_t lds, uint64_t mask)
+{
+    uint64_t save;
+    asm volatile("s_mov_b64 %0, exec\n\ts_mov_b64 exec, %4\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %1, %2\n\ts_mov_b64 exec, %0"
+                 : "=&s"(save)
+                 : "v"(voff), "s"(sbase), "s"(lds), "s"(mask)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4_s(const void* sbase, uint32_t voff, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 __device__ __forceinline__ uint32_t lds_addr(const void* p)
 {
@@ -663,7 +685,7 @@ struct GemmSlot {
     static constexpr int W = Q8 ? 2048 : 1024;               // per wave: [block][32 rows][QSB]
     static constexpr int WX = 256 * (1 + QH + OFF);          // per wave: d_w [, qh] [, m_w], [block][32 rows]
     static constexpr int BYTES = ACT + FACT + 4 * (W + WX);
-    static constexpr int NSH_REAL = 2 * TT + FACT / 1024;    // shared 1 KB copies per stage
+    static constexpr int NSH_REAL = 2 * TT + 2;              // shared copies per stage: codes, then 2 of operands
     static constexpr int SHARED = (NSH_REAL + 3) / 4;        // per wave (the last wave may repeat one)
     static constexpr int OWN = (Q8 ? 2 : 1) + 1 + QH + OFF;  // each wave's own copies per stage
     static constexpr int PER_STAGE = SHARED + OWN;
@@ -736,63 +758,141 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     const int tt0 = tg * TT;
     const int nstages = (B + 1) >> 1;
 
+    // ---- the copy plan. Every copy of a stage is a scalar base that advances by a fixed
+    // stride per stage plus a per-lane 32-bit offset fixed for the kernel, so issuing a stage
+    // costs no vector instructions and no branches. The activation arrays share one
+    // allocation (codes, d_a, d_a·Σq, conversion columns: act_q8_view) and are addressed
+    // from the codes' base.
+    const uint8_t* const abase = reinterpret_cast<const uint8_t*>(a.q);
+    const int64_t ld = (int64_t)a.Tpad;
+    const uint8_t* sh_base[L::SHARED];
+    int64_t sh_stride[L::SHARED];
+    uint32_t sh_voff[L::SHARED], sh_lds[L::SHARED];
+    uint64_t sh_mask[L::SHARED];
+#pragma unroll
+    for (int k = 0; k < L::SHARED; k++) {
+        int i = wave + 4 * k;
+        if (i >= L::NSH_REAL) i = 0;  // padding: repeat copy 0 (same bytes, same place)
+        if (i < 2 * TT) {
+            // activation codes of (tile u, block bb): 64 lanes × 16 B
+            const int u = i >> 1, bb = i & 1;
+            const int tile = tt0 + u < ntt ? tt0 + u : ntt - 1;
+            sh_base[k] = abase + ((int64_t)tile * B + bb) * 1024;
+            sh_stride[k] = 2048;
+            sh_voff[k] = lane * 16;
+            sh_lds[k] = i * 1024;
+            sh_mask[k] = ~0ull;
+        } else {
+            // per-token operands, [block][TT·32 tokens] each in the slot: conversion columns
+            // (8 B), d_a, d_a·Σq (4 B; d_a again when there is no offset term). Copy f = 0
+            // brings the columns, f = 1 the two float arrays; at TT = 2 each fills 64 lanes ×
+            // 16 B, at TT = 1 each fills one half of a 1 KB region (the other lanes masked off)
+            const int f = i - 2 * TT;
+            const int P = TT == 2 ? f * 1024 + lane * 16 : lane * 16;  // byte in the operand region
+            int e;
+            const uint8_t* arr;
+            if (P < L::CV) {
+                e = P / 8, arr = reinterpret_cast<const uint8_t*>(a.cv);
+            } else if (P < L::CV + L::DA) {
+                e = (P - L::CV) / 4, arr = reinterpret_cast<const uint8_t*>(a.d);
+            } else {
+                e = (P - L::CV - L::DA) / 4, arr = reinterpret_cast<const uint8_t*>(OFF ? a.ds : a.d);
+            }
+            const int esize = f == 0 ? 8 : 4;
+            const int bb = e / (TT * 32);
+            int tok = e % (TT * 32);
+            if ((tok >> 5) >= ntt - tt0) tok &= 31;  // a token tile past the end rereads tile tt0
+            sh_base[k] = abase;
+            sh_stride[k] = 2 * ld * esize;
+            sh_voff[k] = (uint32_t)(arr - abase) + (uint32_t)(((int64_t)bb * ld + tt0 * 32 + tok) * esize);
+            sh_lds[k] = 2 * TT * 1024 + (TT == 2 ? f * 1024 : 0);
+            sh_mask[k] = TT == 2 ? ~0ull : (f == 0 ? 0x00000000FFFFFFFFull : 0xFFFFFFFF00000000ull);
+        }
+    }
+    const uint32_t w_voff = Q8 ? lane * 16 : h * 512 + j * 16;
+    const uint32_t x_voff = (h * 32 + j) * 4;
+    const uint32_t ring_lds = lds_addr(ring);
+
     // ---- issue the copies of stage sidx into ring slot `slot`
-    auto issue = [&](int sidx, int slot) {
+    auto issue_fast = [&](int sidx, int slot) {
+        const uint32_t slot_lds = ring_lds + slot * L::BYTES;
+#pragma unroll
+        for (int k = 0; k < L::SHARED; k++) {
+            if (TT == 1)
+                lds_copy16_s_masked(sh_base[k] + sidx * sh_stride[k], sh_voff[k], slot_lds + sh_lds[k], sh_mask[k]);
+            else
+                lds_copy16_s(sh_base[k] + sidx * sh_stride[k], sh_voff[k], slot_lds + sh_lds[k]);
+        }
+        // own copies: weight bytes of blocks 2s, 2s+1 and the per-row factors (d_w [, qh] [, m_w])
+        const uint32_t wlds = slot_lds + L::ACT + L::FACT + wave * L::W;
+        const uint32_t xlds = slot_lds + L::ACT + L::FACT + 4 * L::W + wave * L::WX;
+        const int64_t rb = (int64_t)rtl * B + 2 * sidx;  // first block of the stage in the tile's records
+        if constexpr (Q8) {
+            lds_copy16_s(wqs + rb * 1024, w_voff, wlds);
+            lds_copy16_s(wqs + (rb + 1) * 1024, w_voff, wlds + 1024);
+        } else {
+            lds_copy16_s(wqs + rb * 512, w_voff, wlds);
+        }
+        lds_copy4_s(wd + rb * 32, x_voff, xlds);
+        if (QH) lds_copy4_s(wqh + rb * 32, x_voff, xlds + 256);
+        if (OFF) lds_copy4_s(wm + rb * 32, x_voff, xlds + 256 * (1 + QH));
+    };
+    // The last stage of an odd block count: its second block does not exist, and each copy
+    // rereads block B−1 in its place (per-lane 64-bit addresses; runs once per kernel).
+    auto issue_last_odd = [&](int sidx, int slot) {
         uint8_t* base = ring + slot * L::BYTES;
+        const int blk = B - 1;
+        // the lane index laundered here, so that nothing below is hoisted out of this rare
+        // path and kept live (in registers) across the K loop
+        int lane = threadIdx.x & 63;
+        asm volatile("" : "+v"(lane));
+        const int j = lane & 31;
 #pragma unroll
         for (int k = 0; k < L::SHARED; k++) {
             int i = wave + 4 * k;
-            if (i >= L::NSH_REAL) i = 0;  // padding: repeat copy 0 (same bytes, same place)
+            if (i >= L::NSH_REAL) i = 0;
             if (i < 2 * TT) {
-                // activation codes of (tile u, block bb): 64 lanes × 16 B
-                const int u = i >> 1, bb = i & 1;
+                const int u = i >> 1;
                 const int tile = tt0 + u < ntt ? tt0 + u : ntt - 1;
-                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
                 lds_copy16(a.q + ((int64_t)tile * B + blk) * 1024 + lane * 16, lds_addr(base + i * 1024));
             } else {
-                // per-token operands: lane's 16 bytes at FACT offset o — two conversion
-                // columns, or four floats of d_a or d_a·Σq (d_a again when there is no offset
-                // term)
-                const int o = ((i - 2 * TT) * 64 + lane) * 16;
-                const int64_t ld = (int64_t)a.Tpad;
-                const void* src;
+                const int f = i - 2 * TT;
+                const int P = TT == 2 ? f * 1024 + lane * 16 : lane * 16;
+                const bool mine = TT == 2 || (f == 0) == (lane < 32);
                 int e;
-                if (o < L::CV) {
-                    e = o / 8;
-                } else if (o < L::CV + L::DA) {
-                    e = (o - L::CV) / 4;
+                const uint8_t* arr;
+                if (P < L::CV) {
+                    e = P / 8, arr = reinterpret_cast<const uint8_t*>(a.cv);
+                } else if (P < L::CV + L::DA) {
+                    e = (P - L::CV) / 4, arr = reinterpret_cast<const uint8_t*>(a.d);
                 } else {
-                    e = (o - L::CV - L::DA) / 4;
+                    e = (P - L::CV - L::DA) / 4, arr = reinterpret_cast<const uint8_t*>(OFF ? a.ds : a.d);
                 }
-                const int bb = e / (TT * 32);
+                const int esize = f == 0 ? 8 : 4;
                 int tok = e % (TT * 32);
-                if ((tok >> 5) >= ntt - tt0) tok &= 31;  // a token tile past the end rereads tile tt0
-                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
-                const int64_t idx = blk * ld + tt0 * 32 + tok;
-                if (o < L::CV) src = a.cv + idx;
-                else if (o < L::CV + L::DA || !OFF) src = a.d + idx;
-                else src = a.ds + idx;
-                lds_copy16(src, lds_addr(base + i * 1024));
+                if ((tok >> 5) >= ntt - tt0) tok &= 31;
+                if (mine)
+                    lds_copy16(arr + ((int64_t)blk * ld + tt0 * 32 + tok) * esize,
+                               lds_addr(base + 2 * TT * 1024 + (TT == 2 ? f * 1024 : 0)));
             }
         }
-        // own copies: weight bytes of blocks 2s, 2s+1 (a block past B rereads block B−1)
         uint8_t* wbase = base + L::ACT + L::FACT + wave * L::W;
         uint8_t* xbase = base + L::ACT + L::FACT + 4 * L::W + wave * L::WX;
         if constexpr (Q8) {
 #pragma unroll
-            for (int bb = 0; bb < 2; bb++) {
-                const int blk = 2 * sidx + bb < B ? 2 * sidx + bb : B - 1;
+            for (int bb = 0; bb < 2; bb++)
                 lds_copy16(wqs + ((int64_t)rtl * B + blk) * 1024 + lane * 16, lds_addr(wbase + bb * 1024));
-            }
         } else {
-            const int blk = 2 * sidx + h < B ? 2 * sidx + h : B - 1;
             lds_copy16(wqs + ((int64_t)rtl * B + blk) * 512 + j * 16, lds_addr(wbase));
         }
-        const int blk = 2 * sidx + h < B ? 2 * sidx + h : B - 1;
         const int64_t rec = ((int64_t)rtl * B + blk) * 32 + j;
         lds_copy4(wd + rec, lds_addr(xbase));
         if (QH) lds_copy4(wqh + rec, lds_addr(xbase + 256));
         if (OFF) lds_copy4(wm + rec, lds_addr(xbase + 256 * (1 + QH)));
+    };
+    auto issue = [&](int sidx, int slot) {
+        if (2 * sidx + 1 < B) issue_fast(sidx, slot);
+        else issue_last_odd(sidx, slot);
     };
 
     v16f acc[TT];
