@@ -957,14 +957,21 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     for (int p = 0; p < NS - 1 && p < nstages; p++) issue(p, p);
     // Stage sidx lives in ring slot sidx % NS; the loop below runs whole rounds of the ring
     // with the slot a compile-time constant, so every LDS address is a fixed offset.
-    auto stage = [&](int sidx, auto slot_c) {
+    // STEADY: a stage at least NS stages before the end, whose wait and copy issue need no
+    // checks (the stage it issues is never the odd last one).
+    auto stage = [&](int sidx, auto slot_c, auto steady_c) {
         constexpr int SLOT = decltype(slot_c)::value;
-        // stages issued after this one: NS − 2 in the steady state, fewer at the end
-        const int ahead = nstages - 1 - sidx;
-        if (ahead >= 2) wait_copies_barrier<2 * L::PER_STAGE>();
-        else if (ahead == 1) wait_copies_barrier<L::PER_STAGE>();
-        else wait_copies_barrier<0>();
-        if (sidx + NS - 1 < nstages) issue(sidx + NS - 1, (SLOT + NS - 1) % NS);
+        if constexpr (decltype(steady_c)::value) {
+            wait_copies_barrier<2 * L::PER_STAGE>();
+            issue_fast(sidx + NS - 1, (SLOT + NS - 1) % NS);
+        } else {
+            // stages issued after this one: NS − 2 in the steady state, fewer at the end
+            const int ahead = nstages - 1 - sidx;
+            if (ahead >= 2) wait_copies_barrier<2 * L::PER_STAGE>();
+            else if (ahead == 1) wait_copies_barrier<L::PER_STAGE>();
+            else wait_copies_barrier<0>();
+            if (sidx + NS - 1 < nstages) issue(sidx + NS - 1, (SLOT + NS - 1) % NS);
+        }
         if (!active) return;
         const uint8_t* base = ring + SLOT * L::BYTES;
         const float* da_s = reinterpret_cast<const float*>(base + L::ACT + L::CV);
@@ -972,18 +979,19 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
         // A block past B (odd B, last stage) holds copies of block B−1: its d_w is taken as 0,
         // so S = 0 and fma(I, 0, acc) leaves acc unchanged (acc is never −0), and the loop body
         // needs no branch.
-        const bool valid1 = 2 * sidx + 1 < B;
+        const bool valid1 = decltype(steady_c)::value || 2 * sidx + 1 < B;
         if constexpr (TT == 2) {
 #pragma unroll
             for (int bb = 0; bb < 2; bb++) {
                 const bool valid = bb == 0 || valid1;
-                const v4i w = weights(base, bb);
-                const v16f G0 = block_sums(base, w, 0, bb);
-                const v16f G1 = block_sums(base, w, 1, bb);
                 const float da = da_s[bb * 64 + lane];
                 float dw = dw_s[bb * 32 + j];
                 dw = valid ? dw : 0.0f;
                 const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                const v4i w = weights(base, bb);
+                const v16f G0 = block_sums(base, w, 0, bb);
+                const v16f G1 = block_sums(base, w, 1, bb);
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     acc[0][r] = fmaf(G0[r], S[r], acc[0][r]);
@@ -995,12 +1003,13 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
                 }
             }
         } else {
-            const v16f G0 = block_sums(base, weights(base, 0), 0, 0);
-            const v16f G1 = block_sums(base, weights(base, 1), 0, 1);
             const float da = da_s[h * 32 + j];
             float dw = dw_s[h * 32 + j];
             dw = (h == 0 || valid1) ? dw : 0.0f;
             const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            const v16f G0 = block_sums(base, weights(base, 0), 0, 0);
+            const v16f G1 = block_sums(base, weights(base, 1), 0, 1);
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G0[r], S[r], acc[0][r]);
             if (OFF) offset_term(base, 0, 0, true);
@@ -1014,16 +1023,26 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     typedef std::integral_constant<int, 1> S1;
     typedef std::integral_constant<int, 2> S2;
     typedef std::integral_constant<int, 3> S3;
+    typedef std::true_type ST;
+    typedef std::false_type CK;
     int sidx = 0;
-    for (; sidx + NS <= nstages; sidx += NS) {
-        stage(sidx, S0());
-        stage(sidx + 1, S1());
-        stage(sidx + 2, S2());
-        stage(sidx + 3, S3());
+    // whole rounds whose every stage is steady (the round's last stage, sidx + 3, issues
+    // stage sidx + 6, which exists and is not the last), then the checked rounds
+    for (; sidx + 2 * NS - 1 <= nstages; sidx += NS) {
+        stage(sidx, S0(), ST());
+        stage(sidx + 1, S1(), ST());
+        stage(sidx + 2, S2(), ST());
+        stage(sidx + 3, S3(), ST());
     }
-    if (sidx < nstages) stage(sidx, S0());
-    if (sidx + 1 < nstages) stage(sidx + 1, S1());
-    if (sidx + 2 < nstages) stage(sidx + 2, S2());
+    for (; sidx + NS <= nstages; sidx += NS) {
+        stage(sidx, S0(), CK());
+        stage(sidx + 1, S1(), CK());
+        stage(sidx + 2, S2(), CK());
+        stage(sidx + 3, S3(), CK());
+    }
+    if (sidx < nstages) stage(sidx, S0(), CK());
+    if (sidx + 1 < nstages) stage(sidx + 1, S1(), CK());
+    if (sidx + 2 < nstages) stage(sidx + 2, S2(), CK());
     const int nv = ntt - tt0 < TT ? ntt - tt0 : TT;
     if constexpr (MODE == GEMM_SWIGLU) {
         // Exchange the accumulators through the (now idle) ring: X[wave][u][r][lane]; then
