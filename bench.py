@@ -319,7 +319,7 @@ def main():
     t_, tt_, mode_ = (int(v) for v in roof_kernel[7:-1].split(","))
     breakdown = {}
     for cls in ["gemm*", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "attention", "k_attn_scores",
-                "k_attn_softmax", "k_attn_pv", "k_attn_softmax_pv", "rmsnorm_quant", "swiglu_quant", "quant_act", "rope_store", "embed",
+                "k_attn_softmax", "k_attn_pv", "k_attn_fused", "rmsnorm_quant", "swiglu_quant", "quant_act", "rope_store", "embed",
                 "gemv"] + sorted(kernels):
         c, cms, cops = model.profile_read(cls)
         if c:

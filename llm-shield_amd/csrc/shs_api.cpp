@@ -1090,19 +1090,19 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
                 HIP_TRY(launch_attn_decode(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head,
                                            c.head_dim, scale, m->max_qc, m->max_keys, scr, ctx, qdim,
                                            cap_on ? nullptr : &ac, m->stream));
+            } else if (m->max_kt <= m->fused_kt) {
+                // every item's scores fit one block's LDS: scores, softmax and values in one
+                // kernel; without capture it writes the o projection's activation codes itself
+                Timed tk(m->prof, "k_attn_fused", 2 * attn_ops, m->stream, "attention");
+                HIP_TRY(launch_attn_fused(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head,
+                                          c.head_dim, scale, ctx, qdim, cap_on ? nullptr : &ac, m->max_kt, m->stream));
             } else {
                 {
                     Timed tk(m->prof, "k_attn_scores", attn_ops, m->stream, "attention");
                     HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(), m->n_chunks,
                                                c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, m->stream));
                 }
-                // without capture, the value step writes the o projection's activation codes itself
-                if (m->max_kt <= m->fused_kt) {
-                    // every item's scores fit one block's LDS: softmax and values in one kernel
-                    Timed tk(m->prof, "k_attn_softmax_pv", attn_ops, m->stream, "attention");
-                    HIP_TRY(launch_attn_softmax_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctx, qdim,
-                                                   cap_on ? nullptr : &ac, m->max_kt, m->stream));
-                } else {
+                {
                     {
                         Timed tk(m->prof, "k_attn_softmax", 0, m->stream, "attention");
                         HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu,

@@ -163,12 +163,12 @@ hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, i
 hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
                           const float* scratch, float* ctx, int ldc, const ActQ8* codes, int* counters, int n_cu,
                           hipStream_t s);
-// Softmax and values fused (replaces launch_attn_softmax + launch_attn_pv): one block per
-// (item, query head) holds the item's scores in kt_cap LDS tiles; every item must have at
-// most kt_cap key tiles, and kt_cap at most attn_fused_kt_limit(the device's LDS per block).
-hipError_t launch_attn_softmax_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
-                                  const float* scratch, const float* pm, float* ctx, int ldc, const ActQ8* codes,
-                                  int kt_cap, hipStream_t s);
+// Scores, softmax and values in one kernel (in place of the three above) for passes whose
+// every item has at most kt_cap key tiles: one block per (item, query head) holds the item's
+// scores in kt_cap LDS tiles; kt_cap at most attn_fused_kt_limit(the device's LDS per block).
+hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
+                             int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
+                             const ActQ8* codes, int kt_cap, hipStream_t s);
 int attn_fused_kt_limit(int max_lds_bytes);
 // Attention for items of at most ATT_DEC_MAX_Q queries (decode), at most 4 query heads per
 // KV head: a score kernel over (item, KV head, 64-key chunk) writing the scores to the

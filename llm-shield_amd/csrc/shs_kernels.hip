@@ -631,6 +631,14 @@ __device__ __forceinline__ void lds_copy4_s(const void* sbase, uint32_t voff, ui
                  : "memory", "m0");
 }
 #pragma clang diagnostic pop
+// A pointer every lane of the wave holds, moved into scalar registers (the saddr operand).
+__device__ __forceinline__ const void* wave_uniform(const void* p)
+{
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p)
 {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)p);
@@ -2348,183 +2356,64 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
                 make_float4(o[sl][4 * g], o[sl][4 * g + 1], o[sl][4 * g + 2], o[sl][4 * g + 3]);
 }
 
-// Softmax and values of one (item, query head) in one block, the item's scores kept in the
-// LDS between the two: each score is read from memory once, e = exp(s − max) is formed once
-// per element, and the division and the value chains read their operands from the LDS.
-//  * softmax phase: thread (j, t) owns residue t of query row j, as in attn_softmax_work —
+// Scores, softmax and values of one (item, query head) in one block, the item's scores kept
+// in the LDS between the phases (MinistralModel.AttendGroup, MinistralModel.cs:372-440, in
+// the floating-point order stated above):
+//  * scores: wave w computes whole 32×32 tiles w, w + 4, … — the eight Dot4 chains on
+//    v_mfma_f32_32x32x2f32 as in attn_scores_work, its q row in registers and its K
+//    operands loaded from global memory three chain steps ahead into a register ring. A K
+//    row is read once per block, and the phase has no barrier. vsum8, the scale and the
+//    row maxima (NaN-propagating, so a NaN score reaches the softmax as a NaN maximum)
+//    follow in registers; the tile goes into the LDS in the softmax layout;
+//  * softmax: thread (j, t) owns residue t of query row j, as in attn_softmax_work —
 //    Σe in Kernels.Softmax's order, then w = e / Σe over the row's LDS copy;
-//  * value phase: wave w runs the ordered FMA chain of 32-dimension slice w over all keys,
-//    V tiles staged in the LDS (double-buffered) and shared by the four slices.
+//  * values: wave w runs the ordered FMA chain of 32-dimension slice w over all keys, its V
+//    elements loaded from global memory two tiles ahead, its weights from the LDS one
+//    tile ahead; no barrier either.
 // LDS: kt_cap score tiles of 1024 floats, [query j][slot][k] with residue t in slot
-// t ^ (j & 7) (conflict-free float4 writes, 2-way float4 reads), then two V tiles.
-// Blocks map to (KV-head group, head in group) so that the group's heads — which read the
-// same V rows — share an XCD and start together: block b runs group 8·(b >> 5) + (b & 7)
-// (groups longest first) and head (b >> 3) & 3 of it.
-constexpr int ATT_V_TILE = 32 * ATT_HD;  // floats of one staged V tile
+// t ^ (j & 7) (conflict-free float4 writes, 2-way float4 reads), then the four waves'
+// 32 row maxima. Blocks map to (KV-head group, head in group) so that the group's heads —
+// which read the same K and V rows — share an XCD and start together: block b runs group
+// 8·(b >> 5) + (b & 7) (groups longest first) and head (b >> 3) & 3 of it.
+constexpr int ATT_RMAX = 4 * 32;  // floats of the row maxima after the score tiles
 
 __device__ __forceinline__ int att_swz(int j, int t) { return j * 32 + ((t ^ (j & 7)) << 2); }
 
-__global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restrict__ vc, int cap,
-                                                           const AttnItem* __restrict__ items, int n_items,
-                                                           int n_head, int n_kv, const float* __restrict__ scratch,
-                                                           const float* __restrict__ pm, float* __restrict__ ctx,
-                                                           int ldc, ActQ8 ao, int kt_cap)
+// The value phase: slice `wave` (32 dimensions) of head `head`, the weights read from the
+// block's LDS score tiles S. Lane (j, h) feeds V[key 2c + h][32·wave + j] as the A operand
+// and w[j][2c + h] as the B operand of step c of a tile, so each v_mfma_f32_32x32x2f32 is
+// two consecutive keys of every chain ctx[j][d] = fma(v, w, ctx[j][d]).
+__device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc, int cap, const AttnItem& it, int kvh,
+                                                   int head, int n_kt, int n_keys, const float* S,
+                                                   float* __restrict__ ctx, int ldc, const ActQ8& ao)
 {
-    extern __shared__ float4 att_lds4[];
-    float* S = reinterpret_cast<float*>(att_lds4);
-    float* Vs = S + (int64_t)kt_cap * 1024;
     const int tid = threadIdx.x;
-    const int b = blockIdx.x;
-    const int g = 8 * (b >> 5) + (b & 7), hg = (b >> 3) & 3;
-    const int group = n_head / n_kv;
-    if (g >= n_items * n_kv || hg >= group) return;  // the whole block leaves
-    const int idx = n_items - 1 - g / n_kv, kvh = g % n_kv;
-    const int head = kvh * group + hg;
-    const AttnItem it = items[idx];
-    const int n_kt = att_tiles(it);
-    const int n_keys = it.pos0 + it.q_count;
-    const int64_t tile0 = it.s_off / 1024 + (int64_t)(kvh * 4 + hg) * n_kt;
-
-    // ---- softmax: e over the scores into the LDS, Σe, then w = e / Σe in place
-    {
-        const int j = tid >> 3, t = tid & 7;
-        const bool qvalid = j < it.q_count;
-        const int nq = it.pos0 + j + 1;
-        const int n8 = nq & ~7;
-        float mx = -INFINITY;
-        bool nan = false;
-        for (int kt = t; kt < n_kt; kt += 8) {
-            const float v = pm[(tile0 + kt) * 32 + j];
-            mx = fmaxf(mx, v);
-            nan = nan || v != v;
-        }
-        mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
-        mx = fmaxf(mx, dpp_f<DPP_XOR2>(mx));
-        mx = fmaxf(mx, dpp_f<DPP_HALF_MIRROR>(mx));
-        {
-            int nn = nan ? 1 : 0;
-            nn |= dpp_i<DPP_XOR1>(nn);
-            nn |= dpp_i<DPP_XOR2>(nn);
-            nn |= dpp_i<DPP_HALF_MIRROR>(nn);
-            nan = nn != 0;
-        }
-        const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);
-        const int64_t rec = (int64_t)j * 32 + t * 4;
-        const int sw = att_swz(j, t);
-        constexpr int NB = 8;  // tiles in flight per thread: one block per CU hides no latency
-        float4 nx[NB], sv[NB];
-        auto load = [&](int kt0) {
-#pragma unroll
-            for (int q = 0; q < NB; q++)
-                nx[q] = kt0 + q < n_kt ? *reinterpret_cast<const float4*>(scratch + (tile0 + kt0 + q) * 1024 + rec)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-        };
-        float lane_sum = 0.0f, tail_e = 0.0f;
-        // Tiles below every valid row's n8 — the smallest is row 0's, (pos0 + 1) & ~7, and
-        // pos0 need not be a multiple of 32 — hold only keys each row sees and sums in the
-        // lane order, with s − max ≤ 0 unless the row is uniform: those tiles take a short
-        // path when no valid row of the wave is uniform. Rows past q_count are never read back.
-        const int full_kt = ((it.pos0 + 1) & ~7) >> 5;
-        const bool fast = !__any(qvalid && uniform);
-        if (qvalid) load(0);
-        for (int kt0 = 0; kt0 < n_kt; kt0 += NB) {
-#pragma unroll
-            for (int q = 0; q < NB; q++) sv[q] = nx[q];
-            if (qvalid && kt0 + NB < n_kt) load(kt0 + NB);
-#pragma unroll
-            for (int q = 0; q < NB; q++) {
-                if (kt0 + q >= n_kt) break;
-                const float sc[4] = {sv[q].x, sv[q].y, sv[q].z, sv[q].w};
-                float e[4];
-                if (fast && kt0 + q < full_kt) {
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        e[k] = det_expf_nonpos(sc[k] - mx);
-                        lane_sum = lane_sum + e[k];
-                    }
-                    *reinterpret_cast<float4*>(S + (kt0 + q) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
-                    continue;
-                }
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    // selects, not branches: the lanes of a row disagree on the key tests
-                    const int key = (kt0 + q) * 32 + t + 8 * k;
-                    const float ex = uniform ? 1.0f : det_expf(sc[k] - mx);
-                    e[k] = qvalid && key < nq ? ex : 0.0f;
-                    lane_sum = key < n8 ? lane_sum + e[k] : lane_sum;
-                    tail_e = key >= n8 && key < nq ? e[k] : tail_e;
-                }
-                *reinterpret_cast<float4*>(S + (kt0 + q) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
-            }
-        }
-        float total = vsum8_lanes(lane_sum);
-#pragma unroll
-        for (int k = 0; k < 7; k++) {
-            const float e = __shfl(tail_e, k, 8);
-            if (n8 + k < nq) total = total + e;
-        }
-        if (qvalid) {
-            // four tiles per round, their reads issued together
-            const float rcp = 1.0f / total;
-            for (int kt0 = 0; kt0 < n_kt; kt0 += 4) {
-                float e[16], w[16];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const int kt = kt0 + q < n_kt ? kt0 + q : kt0;  // past the end: reread, not written
-                    const float4 v = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
-                    e[4 * q] = v.x;
-                    e[4 * q + 1] = v.y;
-                    e[4 * q + 2] = v.z;
-                    e[4 * q + 3] = v.w;
-                }
-                softmax_divide<16>(e, w, total, rcp);
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    if (kt0 + q < n_kt)
-                        *reinterpret_cast<float4*>(S + (kt0 + q) * 1024 + sw) =
-                            make_float4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
-            }
-        }
-    }
-
-    // ---- values: slice `wave` of the head
     const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
-    const float* vb = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD;
-    const int vkey = tid >> 3, vd = 16 * (tid & 7);  // thread tid stages key vkey, dimensions vd .. vd+15
-    // Software-pipelined over the key tiles. After the barrier of iteration kt, tile kt + 1's
-    // V sits in LDS buffer (kt + 1) & 1 and every wave is done reading buffer kt & 1 (tile
-    // kt's operands were read in iteration kt − 1). Iteration kt then writes V(kt + 2) into
-    // buffer kt & 1, starts the global load of V(kt + 4), reads tile kt + 1's MFMA operands,
-    // and issues tile kt's 16 MFMAs — the memory instructions interleaved between them, so
-    // they go out while the matrix pipe is busy, and the barrier never waits on fresh LDS
-    // writes. The body has no branch: past the last tile its stores and reads touch
-    // buffers nobody reads again (all inside the block's LDS), and V rows are clamped.
-    struct VRows {
-        v4f v[4];  // native vectors: a float4 struct copy would go through private memory
-    };
-    struct TileOps {
-        float w[16];  // weights of query j, key 2c + h
+    const float* vbase = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD;
+    const int voff = h * (ATT_HD * 4) + (32 * wave + j) * 4;  // bytes
+    struct VOps {
         float a[16];  // V of key 2c + h, dimension 32·wave + j
     };
-    // Rows past the item's last key (and tiles past the last) read that key's row again:
-    // their weights are exactly 0, so fma(v, 0, ctx) leaves ctx as it is — as for the
-    // in-range keys a query does not see — and the loads carry no branch.
-    auto vload = [&](int kt, VRows& r) {
-        const int kidx = kt * 32 + vkey;
-        const float* src = vb + (int64_t)(kidx < n_keys ? kidx : n_keys - 1) * ATT_HD + vd;
-#pragma unroll
-        for (int x = 0; x < 4; x++) r.v[x] = *reinterpret_cast<const v4f*>(src + 4 * x);
+    struct WOps {
+        float w[16];  // weights of query j, key 2c + h
     };
-    auto vstore = [&](int kt, const VRows& r) {
-        float* vt = Vs + (kt & 1) * ATT_V_TILE;
+    // One buffer resource per tile, whose range ends at the item's last key: rows past it
+    // (and tiles past the last) read as 0 without touching memory. Their weights are 0 as
+    // well, and fma(0, 0, ctx) is ctx (ctx starts at +0 and a sum that starts at +0 is never
+    // −0), as for the in-range keys a query does not see.
+    auto vload = [&](int kt, VOps& op) {
+        const int rows = n_keys - kt * 32;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vbase + (int64_t)kt * 32 * ATT_HD), 0, rows > 0 ? rows * (ATT_HD * 4) : 0, 0x00020000);
 #pragma unroll
-        for (int x = 0; x < 4; x++) *reinterpret_cast<v4f*>(vt + vkey * ATT_HD + vd + 4 * x) = r.v[x];
+        for (int c = 0; c < 16; c++)
+            op.a[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff + c * (2 * ATT_HD * 4), 0, 0));
     };
-    auto oread = [&](int kt, TileOps& op) {
-        // weights: residue 2m + h (m = c & 3), k = c >> 2 of the tile's rows; tile kt_cap
-        // (past the last) reads the first V buffer instead, unused
-        const float* st = S + (kt < kt_cap ? kt : 0) * 1024;
+    auto wread = [&](int kt, WOps& op) {
+        // residue 2m + h (m = c & 3), k = c >> 2 of the tile's rows; past the last tile the
+        // last is read again, unused
+        const float* st = S + min(kt, n_kt - 1) * 1024;
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const float4 v = *reinterpret_cast<const float4*>(st + att_swz(j, 2 * m + h));
@@ -2533,49 +2422,36 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
             op.w[m + 8] = v.z;
             op.w[m + 12] = v.w;
         }
-        const float* vt = Vs + (kt & 1) * ATT_V_TILE;
-#pragma unroll
-        for (int c = 0; c < 16; c++) op.a[c] = vt[(2 * c + h) * ATT_HD + 32 * wave + j];
     };
     v16f o;
 #pragma unroll
     for (int r = 0; r < 16; r++) o[r] = 0.0f;
-    VRows ra, rb;
-    TileOps oa, ob;
-    vload(0, ra);
-    vload(1, rb);
-    vstore(0, ra);
-    vstore(1, rb);
-    vload(2, ra);
-    vload(3, rb);
-    __syncthreads();  // V(0), V(1) staged, and every w written
-    oread(0, oa);
-    // iteration kt: `vs` holds V(kt + 2), `cur` tile kt's operands
-    auto step = [&](int kt, VRows& vs, TileOps& cur, TileOps& nxt) {
-        __syncthreads();
-        vstore(kt + 2, vs);
-        vload(kt + 4, vs);
-        oread(kt + 1, nxt);
+    VOps va, vb;
+    WOps wa, wb;
+    vload(0, va);
+    vload(1, vb);
+    __syncthreads();  // every w is written
+    wread(0, wa);
+    // iteration kt: `cur` holds V(kt) (V(kt + 1) in flight), `w` tile kt's weights; it reads
+    // tile kt + 1's weights, issues tile kt's 16 MFMAs, then loads V(kt + 2) into `cur`
+    auto step = [&](int kt, VOps& cur, WOps& w, WOps& wn) {
+        wread(kt + 1, wn);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int c = 0; c < 16; c++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[c], cur.w[c], o, 0, 0, 0);
-        // one memory instruction after each MFMA (LDS write, global load, LDS read)
-        __builtin_amdgcn_sched_group_barrier(0x0200, 4, 0);
-#pragma unroll
-        for (int c = 0; c < 16; c++) {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x0020 | 0x0100, 1, 0);
-        }
+        for (int c = 0; c < 16; c++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[c], w.w[c], o, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        vload(kt + 2, cur);
     };
-    // whole pairs, then the odd tile: every path into the loop head carries the same
-    // outstanding loads (V(kt + 2), then V(kt + 3)), so each store waits for its own alone
     int kt = 0;
     for (; kt + 1 < n_kt; kt += 2) {
-        step(kt, ra, oa, ob);
-        step(kt + 1, rb, ob, oa);
+        step(kt, va, wa, wb);
+        step(kt + 1, vb, wb, wa);
     }
-    if (kt < n_kt) step(kt, ra, oa, ob);
+    if (kt < n_kt) step(kt, va, wa, wb);
     if (ao.q) {
-        // the o projection's quantization, as in attn_pv_work
+        // The o projection's quantization of ctx, fused: the slice is one 32-dimension block
+        // of query j, in the layout quant_block_pair takes. Rows past the item's queries are
+        // not written (they belong to the next item, or are padding the GEMM never stores).
         if (j < it.q_count) {
             float y[16];
 #pragma unroll
@@ -2589,6 +2465,191 @@ __global__ __launch_bounds__(256, 1) void k_attn_softmax_pv(const float* __restr
 #pragma unroll
     for (int gq = 0; gq < 4; gq++)
         *reinterpret_cast<float4*>(outp + 8 * gq + 4 * h) = make_float4(o[4 * gq], o[4 * gq + 1], o[4 * gq + 2], o[4 * gq + 3]);
+}
+
+__global__ __launch_bounds__(256, 1) void k_attn_fused(const float* __restrict__ q, int ldq,
+                                                      const float* __restrict__ kc, const float* __restrict__ vc,
+                                                      int cap, const AttnItem* __restrict__ items, int n_items,
+                                                      int n_head, int n_kv, float scale, float* __restrict__ ctx,
+                                                      int ldc, ActQ8 ao, int kt_cap)
+{
+    extern __shared__ float4 att_lds4[];
+    float* S = reinterpret_cast<float*>(att_lds4);
+    float* rmax = S + (int64_t)kt_cap * 1024;  // [wave][query row] maxima of the score phase
+    const int tid = threadIdx.x;
+    const int b = blockIdx.x;
+    const int g = 8 * (b >> 5) + (b & 7), hg = (b >> 3) & 3;
+    const int group = n_head / n_kv;
+    if (g >= n_items * n_kv || hg >= group) return;  // the whole block leaves
+    const int idx = n_items - 1 - g / n_kv, kvh = g % n_kv;
+    const int head = kvh * group + hg;
+    const AttnItem it = items[idx];
+    const int n_kt = att_tiles(it);
+    const int n_keys = it.pos0 + it.q_count;
+
+    // ---- scores
+    {
+        const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+        const int j = lane & 31, h = lane >> 5;
+        const bool q_ok = j < it.q_count;
+        const int nq = it.pos0 + j + 1;  // keys query j attends to
+        const float* kb = kc + ((int64_t)kvh * cap + it.key_start) * ATT_HD + 8 * h;
+        // A operands: row i of the A tile carries key kap(i), so D row i holds key kap(i),
+        // and register r of lane half h holds key 2r + h
+        const int kap = 8 * (j >> 3) + 2 * (j & 3) + ((j >> 2) & 1);
+        // B operands: step s of chain l needs q[l + 16s + 8h]; qv[s] holds l = 0..7
+        v4f qv[8][2];
+        {
+            const float* qrow = q + (int64_t)(it.q_start + (q_ok ? j : 0)) * ldq + head * ATT_HD + 8 * h;
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int x = 0; x < 2; x++)
+                    qv[s][x] = q_ok ? *reinterpret_cast<const v4f*>(qrow + 16 * s + 4 * x) : v4f{0.f, 0.f, 0.f, 0.f};
+        }
+        // K operands of step s of tile kt: k[l + 16s + 8h] of key kap, l = 0..7; rows past
+        // the item's last key read that key (their scores are masked)
+        auto kload = [&](int kt, int s, v4f (&k)[2]) {
+            const float* src = kb + (int64_t)min(kt * 32 + kap, n_keys - 1) * ATT_HD + 16 * s;
+            k[0] = *reinterpret_cast<const v4f*>(src);
+            k[1] = *reinterpret_cast<const v4f*>(src + 4);
+        };
+        const int n_mine = n_kt > wave ? (n_kt - wave + 3) >> 2 : 0;  // tiles wave, wave + 4, ...
+        const int last = wave + 4 * (n_mine > 0 ? n_mine - 1 : 0);
+        float mx = -INFINITY;
+        v4f kr[4][2];  // ring: step g of the wave's step sequence in slot g & 3, loaded 3 steps ahead
+        if (n_mine > 0) {
+            kload(wave, 0, kr[0]);
+            kload(wave, 1, kr[1]);
+            kload(wave, 2, kr[2]);
+        }
+        for (int u = 0; u < n_mine; u++) {
+            const int kt = wave + 4 * u;
+            const int ktn = min(kt + 4, last);  // the wave's next tile; its last tile repeats
+            v16f c[8];
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                if (s < 5) kload(kt, s + 3, kr[(s + 3) & 3]);
+                else kload(ktn, s - 5, kr[(s + 3) & 3]);
+                // the loads go out before this step's MFMAs
+                __builtin_amdgcn_sched_barrier(0);
+                const v4f k0 = kr[s & 3][0], k1 = kr[s & 3][1];
+                const v16f z = {};
+                // the 8 chains advance together: step s is 8 independent MFMAs
+                c[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.x, qv[s][0].x, s ? c[0] : z, 0, 0, 0);
+                c[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.y, qv[s][0].y, s ? c[1] : z, 0, 0, 0);
+                c[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.z, qv[s][0].z, s ? c[2] : z, 0, 0, 0);
+                c[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.w, qv[s][0].w, s ? c[3] : z, 0, 0, 0);
+                c[4] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.x, qv[s][1].x, s ? c[4] : z, 0, 0, 0);
+                c[5] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.y, qv[s][1].y, s ? c[5] : z, 0, 0, 0);
+                c[6] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.z, qv[s][1].z, s ? c[6] : z, 0, 0, 0);
+                c[7] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.w, qv[s][1].w, s ? c[7] : z, 0, 0, 0);
+            }
+            float sc[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                // vsum8 of the chains, then the scale
+                const float a = (c[0][r] + c[1][r]) + (c[2][r] + c[3][r]);
+                const float bsum = (c[4][r] + c[5][r]) + (c[6][r] + c[7][r]);
+                sc[r] = (a + bsum) * scale;
+            }
+            // residue 2m + h of query j is (sc[m], sc[m+4], sc[m+8], sc[m+12])
+            float* out = S + kt * 1024;
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                *reinterpret_cast<float4*>(out + att_swz(j, 2 * m + h)) =
+                    make_float4(sc[m], sc[m + 4], sc[m + 8], sc[m + 12]);
+            if ((kt + 1) * 32 <= it.pos0 + 1) {
+                // below every row's first masked key; rows past q_count are never read back
+#pragma unroll
+                for (int r = 0; r < 16; r += 2)
+                    mx = __builtin_elementwise_maximum(mx, __builtin_elementwise_maximum(sc[r], sc[r + 1]));
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    mx = __builtin_elementwise_maximum(mx, q_ok && kt * 32 + 2 * r + h < nq ? sc[r] : -INFINITY);
+            }
+        }
+        // the ring's loads past the wave's last tile are still in flight
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        mx = __builtin_elementwise_maximum(mx, __shfl_xor(mx, 32));
+        if (h == 0) rmax[wave * 32 + j] = mx;
+        __syncthreads();  // every score and maximum is written
+    }
+
+    // ---- softmax: e in place, Σe, then w = e / Σe in place
+    {
+        const int j = tid >> 3, t = tid & 7;
+        const bool qvalid = j < it.q_count;
+        const int nq = it.pos0 + j + 1;
+        const int n8 = nq & ~7;
+        const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(rmax[j], rmax[32 + j]),
+                                                       __builtin_elementwise_maximum(rmax[64 + j], rmax[96 + j]));
+        const bool nan = mx != mx;
+        const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);
+        const int sw = att_swz(j, t);
+        float lane_sum = 0.0f, tail_e = 0.0f;
+        const int full_kt = ((it.pos0 + 1) & ~7) >> 5;
+        const bool fast = !__any(qvalid && uniform);
+        constexpr int NB = 4;
+        for (int kt0 = 0; kt0 < n_kt; kt0 += NB) {
+            float4 sv[NB];
+#pragma unroll
+            for (int qq = 0; qq < NB; qq++)
+                sv[qq] = *reinterpret_cast<const float4*>(S + (kt0 + qq < n_kt ? kt0 + qq : kt0) * 1024 + sw);
+#pragma unroll
+            for (int qq = 0; qq < NB; qq++) {
+                if (kt0 + qq >= n_kt) break;
+                const float sc[4] = {sv[qq].x, sv[qq].y, sv[qq].z, sv[qq].w};
+                float e[4];
+                if (fast && kt0 + qq < full_kt) {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        e[k] = det_expf_nonpos(sc[k] - mx);
+                        lane_sum = lane_sum + e[k];
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int key = (kt0 + qq) * 32 + t + 8 * k;
+                        const float ex = uniform ? 1.0f : det_expf(sc[k] - mx);
+                        e[k] = qvalid && key < nq ? ex : 0.0f;
+                        lane_sum = key < n8 ? lane_sum + e[k] : lane_sum;
+                        tail_e = key >= n8 && key < nq ? e[k] : tail_e;
+                    }
+                }
+                *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
+            }
+        }
+        float total = vsum8_lanes(lane_sum);
+#pragma unroll
+        for (int k = 0; k < 7; k++) {
+            const float e = __shfl(tail_e, k, 8);
+            if (n8 + k < nq) total = total + e;
+        }
+        if (qvalid) {
+            const float rcp = 1.0f / total;
+            for (int kt0 = 0; kt0 < n_kt; kt0 += 4) {
+                float e[16], w[16];
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++) {
+                    const int kt = kt0 + qq < n_kt ? kt0 + qq : kt0;  // past the end: reread, not written
+                    const float4 v = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
+                    e[4 * qq] = v.x;
+                    e[4 * qq + 1] = v.y;
+                    e[4 * qq + 2] = v.z;
+                    e[4 * qq + 3] = v.w;
+                }
+                softmax_divide<16>(e, w, total, rcp);
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++)
+                    if (kt0 + qq < n_kt)
+                        *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) =
+                            make_float4(w[4 * qq], w[4 * qq + 1], w[4 * qq + 2], w[4 * qq + 3]);
+            }
+        }
+    }
+    attn_values_stream(vc, cap, it, kvh, head, n_kt, n_keys, S, ctx, ldc, ao);
 }
 
 // The softmax and value kernels of the three-kernel path take their work longest first
@@ -2693,30 +2754,30 @@ hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n
 
 int attn_fused_kt_limit(int max_lds_bytes)
 {
-    const int kt = (max_lds_bytes - 2 * ATT_V_TILE * (int)sizeof(float)) / (1024 * (int)sizeof(float));
+    const int kt = (max_lds_bytes - ATT_RMAX * (int)sizeof(float)) / (1024 * (int)sizeof(float));
     return kt > 0 ? kt : 0;
 }
 
-hipError_t launch_attn_softmax_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
-                                  const float* scratch, const float* pm, float* ctx, int ldc, const ActQ8* codes,
-                                  int kt_cap, hipStream_t s)
+hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
+                             int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
+                             const ActQ8* codes, int kt_cap, hipStream_t s)
 {
     if (n_items <= 0) return hipSuccess;
-    if (n_head % n_kv != 0 || n_head / n_kv > 4 || kt_cap <= 0) return hipErrorInvalidValue;
+    if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4 || kt_cap <= 0) return hipErrorInvalidValue;
     if (codes && (codes->B != n_head * ATT_HD / 32 || !codes->q)) return hipErrorInvalidValue;
     const ActQ8 ao = codes ? *codes : ActQ8();
-    const size_t lds = ((size_t)kt_cap * 1024 + 2 * ATT_V_TILE) * sizeof(float);
+    const size_t lds = ((size_t)kt_cap * 1024 + ATT_RMAX) * sizeof(float);
     static int attr_set = 0;
     if (attr_set < (int)lds) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_softmax_pv),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_fused),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         attr_set = (int)lds;
     }
     const int n_groups = n_items * n_kv;
     const unsigned grid = (unsigned)(((n_groups + 7) / 8) * 32);
-    hipLaunchKernelGGL(k_attn_softmax_pv, dim3(grid), dim3(256), lds, s, vc, cap, items, n_items, n_head, n_kv, scratch,
-                       pm, ctx, ldc, ao, kt_cap);
+    hipLaunchKernelGGL(k_attn_fused, dim3(grid), dim3(256), lds, s, q, ldq, kc, vc, cap, items, n_items, n_head, n_kv,
+                       scale, ctx, ldc, ao, kt_cap);
     return hipGetLastError();
 }
 

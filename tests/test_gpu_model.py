@@ -52,13 +52,15 @@ def test_forward_matches_oracle_and_first_layer_is_bit_exact(shs, oracle, tiny):
 
 def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
     """A pass whose longest 32-query item has at most as many key tiles as one block's LDS
-    holds runs softmax and values fused; a longer one (here 1100 keys, past 1024) takes the
-    three-kernel path. Both are bit-exact, including a pass that starts mid-tile."""
+    holds (39 tiles of 32 keys in 160 KB) runs scores, softmax and values in one kernel
+    (k_attn_fused); a longer one (here 1300 keys) takes the three-kernel path. Both are
+    bit-exact, including a pass that starts mid-tile and one at the fused kernel's limit
+    (1240 keys: 39 tiles, the last partial)."""
     cfg, tensors, types, gpu, ora = tiny
-    long_ora = oracle.OracleModel(cfg, tensors, types, cap=1200)
+    long_ora = oracle.OracleModel(cfg, tensors, types, cap=1400)
     rng = np.random.default_rng(11)
     ids = [1, 200, 511]
-    for prefix, n, fused in ((0, 70, True), (45, 50, True), (0, 1100, False)):
+    for prefix, n, fused in ((0, 70, True), (45, 50, True), (0, 1240, True), (0, 1300, False)):
         toks = rng.integers(0, cfg.vocab, prefix + n)
         gpu.reset_kv_cache()
         long_ora.reset()
@@ -69,7 +71,7 @@ def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
         gpu.profile_reset()
         try:
             g = gpu.forward_selected(toks[prefix:], ids)
-            n_fused = gpu.profile_read("k_attn_softmax_pv")[0]
+            n_fused = gpu.profile_read("k_attn_fused")[0]
             n_split = gpu.profile_read("k_attn_softmax")[0]
         finally:
             gpu.profile(False)
@@ -80,23 +82,23 @@ def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
 
 def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
     """GQA groups below 4: the score kernel leaves a block's extra waves idle and the fused
-    softmax + values kernel skips the missing heads' blocks; both attention paths stay
-    bit-exact (a 40-token pass and a 1100-token one)."""
+    kernel skips the missing heads' blocks; both attention paths stay bit-exact (40- and
+    1100-token passes take the fused kernel, a 1300-token one the three-kernel path)."""
     cfg = oracle.make_config(n_layer=1, hidden=256, n_head=4, n_kv_head=2, head_dim=128, ffn=512, vocab=512)
     tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=13)
     gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types)
-    ora = oracle.OracleModel(cfg, tensors, types, cap=1200)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=1400)
     rng = np.random.default_rng(17)
     ids = [0, 77, 300]
     try:
-        for n in (40, 1100):
+        for n in (40, 1100, 1300):
             toks = rng.integers(0, cfg.vocab, n)
             gpu.reset_kv_cache()
             ora.reset()
             g = gpu.forward_selected(toks, ids)
             o = ora.forward(toks, head_mode=1, vocab_ids=ids)
             assert np.array_equal(g, o), (n, H.rel_l2(g, o))
-        # decode width onto the 1100-token cache: 2 queries, then 1 (k_attn_dec_scores + k_attn_dec_pv)
+        # decode width onto the 1300-token cache: 2 queries, then 1 (k_attn_dec_scores + k_attn_dec_pv)
         gpu.profile(True)
         gpu.profile_reset()
         try:
