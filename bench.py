@@ -230,6 +230,46 @@ def decode_main(args):
     return 0
 
 
+# Instruction-issue probes (llm-shield_amd/libshs_probe.so): pattern name, what one iteration
+# issues, and the instruction each per-instruction figure divides by.
+ISA_PATTERNS = [
+    ("i8", "4 independent v_mfma_i32_32x32x32_i8", 4),
+    ("f16x8", "4 independent v_mfma_f32_32x32x8_f16", 4),
+    ("f16x16", "4 independent v_mfma_f32_32x32x16_f16", 4),
+    ("f32_1_2b", "2 v_mfma_f32_32x32x1_2b_f32, C = 0 (the GEMM's scale)", 2),
+    ("f32x2", "2 independent v_mfma_f32_32x32x2_f32 (the attention's chains)", 2),
+    ("fma", "32 independent v_fma_f32", 32),
+    ("i8+fma", "2 int8 MFMAs + 32 independent FMAs", None),
+    ("f16+fma", "2 fp16 x8 MFMAs + 32 independent FMAs", None),
+    ("f32+fma", "1 fp32 1_2b MFMA + 32 independent FMAs", None),
+    ("gemm_block", "one GEMM block on two token tiles: scale, 2 int8, 2 fp16, 32 dependent FMAs", None),
+]
+
+
+def isa_probe(iters=20000):
+    """SIMD cycles per iteration of each probe pattern (shader clock, from the span of each
+    work-group's waves), for one wave per SIMD on one CU and for three waves per SIMD on every
+    CU (the GEMM's occupancy)."""
+    import ctypes as C
+    lib = C.CDLL(str(ROOT / "llm-shield_amd" / "libshs_probe.so"))
+    assert lib.shs_probe_count() == len(ISA_PATTERNS)
+    rows = []
+    for p, (name, what, per) in enumerate(ISA_PATTERNS):
+        row = {"pattern": name, "issues": what}
+        for label, blocks, waves in (("1_wave_per_simd", 1, 4), ("3_waves_per_simd_all_cus", 256, 12)):
+            cyc, mhz = C.c_double(), C.c_double()
+            rc = lib.shs_probe_run(p, blocks, waves, iters, C.byref(cyc), C.byref(mhz))
+            if rc != 0:
+                raise RuntimeError(f"probe {name}: HIP error {rc}")
+            e = {"simd_cycles_per_iter": round(cyc.value, 1), "clock_mhz": round(mhz.value)}
+            if per:
+                e["simd_cycles_per_instruction"] = round(cyc.value / per, 2)
+            row[label] = e
+        rows.append(row)
+    print(json.dumps({"isa_probe": rows, "iters": iters}), flush=True)
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,6 +282,8 @@ def main():
                     help="time without the per-kernel HIP events (no roofline or breakdown)")
     ap.add_argument("--copy-probe", action="store_true",
                     help=f"first copy {COPY_PROBE_BYTES >> 20} MiB device to device (counter calibration)")
+    ap.add_argument("--isa-probe", action="store_true",
+                    help="print the issue cost of each MFMA / VALU form the GEMM uses and exit")
     ap.add_argument("--decode", action="store_true",
                     help=f"measure decode instead: --steps single-token forwards onto a {DECODE_CONTEXT}-token context")
     args = ap.parse_args()
@@ -249,6 +291,8 @@ def main():
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the verdict path does not shard "
               f"across GPUs in this build.", file=sys.stderr)
         return 2
+    if args.isa_probe:
+        return isa_probe()
     if args.decode:
         return decode_main(args)
 
