@@ -201,8 +201,10 @@ shs_status shs_synchronize(shs_model* model);
  * gemm_gate_up, gemm_down, gemm_head, gemv, attention, rmsnorm_quant, swiglu_quant,
  * quant_act, rope_store, embed; and by kernel, under the names rocprofv3 reports:
  * "k_gemm<type,TT,mode>" (each GEMM launch is in both), k_attn_scores, k_attn_softmax,
- * k_attn_pv. kernel_class "prefix*" sums the classes with that prefix. total_ops is the
- * algorithmic operation count (2·tokens·rows·cols for a GEMM, 0 where not counted). */
+ * k_attn_pv, k_attn_fused. kernel_class "prefix*" sums the classes with that prefix.
+ * total_ops is the algorithmic operation count (2·tokens·rows·cols for a GEMM), for
+ * rmsnorm_quant the algorithmic HBM bytes (the rows read, their int8 codes and per-block
+ * d, d·Σq and conversion column written), 0 where not counted. */
 shs_status shs_profile_enable(shs_model* model, int32_t enable);
 shs_status shs_profile_read(shs_model* model, const char* kernel_class, int64_t* launches,
                             double* total_ms, double* total_ops);

@@ -285,6 +285,14 @@ struct Profiler {
 };
 
 // RAII scope that times one launch when profiling is on.
+// Algorithmic HBM bytes of one RMSNorm + quantization launch over `rows` rows of n: the
+// rows and the gains read, the int8 codes and per 32-block d, d·Σq and the 8-byte
+// conversion column written.
+static double rmsnorm_bytes(int rows, int n)
+{
+    return (double)rows * n * 4.0 + (double)n * 4.0 + (double)rows * n + (double)rows * (n / 32) * 16.0;
+}
+
 struct Timed {
     Profiler& p;
     hipStream_t s;
@@ -1033,7 +1041,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         const bool qkv_norm = qkv_fused && gemm_narrow_tokens(L.qkv.parts[0], ah, GEMM_QKV, true) > 0;
         const bool gu_norm = gu_fused && gemm_narrow_tokens(L.gu.parts[0], ah, GEMM_SWIGLU, true) > 0;
         if (!qkv_norm) {
-            Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
+            Timed tm(m->prof, "rmsnorm_quant", rmsnorm_bytes(T, hidden), m->stream);
             HIP_TRY(launch_rmsnorm_quant(h, hidden, L.attn_norm, c.rms_eps, hidden, ah, normed, m->stream));
         }
         snprintf(name, sizeof name, "blk.%d.attn_norm", l);
@@ -1135,7 +1143,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
         }
 
         if (!gu_norm) {
-            Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
+            Timed tm(m->prof, "rmsnorm_quant", rmsnorm_bytes(T, hidden), m->stream);
             HIP_TRY(launch_rmsnorm_quant(h, hidden, L.ffn_norm, c.rms_eps, hidden, ah, normed, m->stream));
         }
         snprintf(name, sizeof name, "blk.%d.ffn_norm", l);
@@ -1193,7 +1201,7 @@ shs_status run_head(shs_model* m, const std::vector<int32_t>& rows, int head_mod
     HIP_TRY(m->act.ensure(n, c.hidden, &a));
     float* normed = m->cap_fn ? m->normed.as<float>() : nullptr;
     {
-        Timed tm(m->prof, "rmsnorm_quant", 0, m->stream);
+        Timed tm(m->prof, "rmsnorm_quant", rmsnorm_bytes(n, c.hidden), m->stream);
         HIP_TRY(launch_rmsnorm_quant(x_in, c.hidden, m->out_norm, c.rms_eps, c.hidden, a, normed, m->stream));
     }
     Capture cp{m, {}};
