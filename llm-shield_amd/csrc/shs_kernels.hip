@@ -457,12 +457,26 @@ __device__ __forceinline__ void rmsnorm_rows(const float* __restrict__ xr, const
     }
 }
 
-// One block of 256 threads per token (padding tokens get zero codes).
+// RMSNorm + quantization of one token row per block of 256 threads (padding tokens get
+// zero codes): Kernels.RmsNorm's arithmetic as rmsnorm_rows states it, laid out for a whole
+// row at once.
+//  * The row's float4s are loaded once; x goes to the LDS row-major and x·x transposed as
+//    sq[s][k] = x²[s + 16k] (rows padded to a multiple of 4 floats plus 4, so the 16 chain
+//    lanes' float4 reads fall in distinct banks).
+//  * Lane s < 16 runs running sum s over k = 0, 1, … in order, reading 4 steps per LDS load,
+//    16 steps ahead of its adds.
+//  * Thread p = 2b + h quantizes half h of block b: elements 8h..8h+7 and 16+8h..16+8h+7,
+//    exactly the 16 code bytes the GEMM's lane half h multiplies, written as one 16-byte
+//    store. The block's max and Σq combine over the lane pair (exact in any order), then
+//    d = max/127, 1/d and the codes follow IntegerGemm.QuantizeActivations as quant_block8.
+constexpr int RMS_SQ_PAD = 4;
+__device__ __forceinline__ int rms_sq_ld(int n) { return (((n >> 4) + 3) & ~3) + RMS_SQ_PAD; }
+
 __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__ x, int ldx,
                                                        const float* __restrict__ w, float eps, int n,
                                                        ActQ8 a, float* __restrict__ y_opt)
 {
-    extern __shared__ float sx[];  // the row, then its squares
+    extern __shared__ float sx[];  // the row, then the transposed squares
     __shared__ float part[16];
     __shared__ float s_scale;
     const int t = blockIdx.x, tid = threadIdx.x;
@@ -470,17 +484,134 @@ __global__ __launch_bounds__(256) void k_rmsnorm_quant(const float* __restrict__
         for (int b = tid >> 3; b < a.B; b += blockDim.x >> 3) zero_block8(tid & 7, a, t, b);
         return;
     }
+    const int nk = n >> 4, ld = rms_sq_ld(n), npair = n >> 4;
+    float* sq = sx + n;
+    const float* xr = x + (int64_t)t * ldx;
+    // the gains of this thread's first pair, loaded now so their latency overlaps the row's
+    float4 wpre[4];
+    if (tid < npair) {
+        const float* wp = w + 32 * (tid >> 1) + 8 * (tid & 1);
+        wpre[0] = *reinterpret_cast<const float4*>(wp);
+        wpre[1] = *reinterpret_cast<const float4*>(wp + 4);
+        wpre[2] = *reinterpret_cast<const float4*>(wp + 16);
+        wpre[3] = *reinterpret_cast<const float4*>(wp + 20);
+    }
+    const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15) == 0) && (ldx & 3) == 0;
+    for (int i = tid; i < n / 4; i += 256) {
+        const float4 v = vec ? reinterpret_cast<const float4*>(xr)[i]
+                             : make_float4(xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]);
+        reinterpret_cast<float4*>(sx)[i] = v;
+        // elements 4i + c: running sum s = 4(i & 3) + c, step k = i >> 2
+        float* d = sq + 4 * (i & 3) * ld + (i >> 2);
+        d[0] = v.x * v.x;
+        d[ld] = v.y * v.y;
+        d[2 * ld] = v.z * v.z;
+        d[3 * ld] = v.w * v.w;
+    }
+    lds_barrier();
+    if (tid < 16) {
+        const float* row = sq + tid * ld;
+        float acc = 0.0f;
+        int k = 0;
+        // 16 steps per group: the next group's four float4 reads are issued before the
+        // current group's 16 adds, which stay one chain in order
+        const int kfull = nk & ~15;
+        if (kfull > 0) {
+            float4 ca[4], cb[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) ca[q] = reinterpret_cast<const float4*>(row)[q];
+            for (; k < kfull; k += 16) {
+                const int kn = k + 16 < kfull ? k + 16 : k;  // past the last group: reread, unused
+#pragma unroll
+                for (int q = 0; q < 4; q++) cb[q] = reinterpret_cast<const float4*>(row + kn)[q];
+                asm volatile("" : "+v"(acc)::"memory");
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc = ((((acc + ca[q].x) + ca[q].y) + ca[q].z) + ca[q].w);
+                asm volatile("" : "+v"(acc)::"memory");
+#pragma unroll
+                for (int q = 0; q < 4; q++) ca[q] = cb[q];
+            }
+        }
+        for (; k < nk; k++) acc = acc + row[k];
+        part[tid] = acc;
+    }
+    lds_barrier();
+    if (tid == 0) {
+        double sum = 0.0;
+        int i = 0;
+        if (n >= 16) {
+            sum = (double)vsum8(part) + (double)vsum8(part + 8);
+            i = n / 16 * 16;
+        }
+        for (; i < n; i++) sum += (double)sx[i] * (double)sx[i];
+        s_scale = 1.0f / sqrtf((float)(sum / n) + eps);
+    }
+    lds_barrier();
+    const float sc = s_scale;
     float* y_row = y_opt ? y_opt + (int64_t)t * n : nullptr;
-    rmsnorm_rows(x + (int64_t)t * ldx, w, eps, n, sx, part, &s_scale, [&](float4 v, int l8, int b) {
-        if (y_row) *reinterpret_cast<float4*>(y_row + 32 * b + 4 * l8) = v;
-        quant_block8(v, l8, a, t, b, 0);
-    }, [] {});
+    for (int p = tid; p < npair; p += 256) {
+        const int b = p >> 1, h = p & 1;
+        const int e0 = 32 * b + 8 * h;
+        float4 wv[4];
+        if (p == tid) {
+            wv[0] = wpre[0], wv[1] = wpre[1], wv[2] = wpre[2], wv[3] = wpre[3];
+        } else {
+            wv[0] = *reinterpret_cast<const float4*>(w + e0);
+            wv[1] = *reinterpret_cast<const float4*>(w + e0 + 4);
+            wv[2] = *reinterpret_cast<const float4*>(w + e0 + 16);
+            wv[3] = *reinterpret_cast<const float4*>(w + e0 + 20);
+        }
+        float v[16];
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 xv = *reinterpret_cast<const float4*>(sx + e0 + 4 * (g & 1) + 16 * (g >> 1));
+            v[4 * g] = (xv.x * sc) * wv[g].x;
+            v[4 * g + 1] = (xv.y * sc) * wv[g].y;
+            v[4 * g + 2] = (xv.z * sc) * wv[g].z;
+            v[4 * g + 3] = (xv.w * sc) * wv[g].w;
+        }
+        if (y_row) {
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4*>(y_row + e0 + 4 * (g & 1) + 16 * (g >> 1)) =
+                    make_float4(v[4 * g], v[4 * g + 1], v[4 * g + 2], v[4 * g + 3]);
+        }
+        // fmaxf drops NaN operands, so a block's max is NaN only when all 32 values are
+        // (as the 8-lane reduction of quant_block8 gives it)
+        float mx = fabsf(v[0]);
+#pragma unroll
+        for (int r = 1; r < 16; r++) mx = fmaxf(mx, fabsf(v[r]));
+        mx = fmaxf(mx, dpp_f<DPP_XOR1>(mx));
+        const float d = mx / 127.0f;
+        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        int q[16];
+        uint32_t usum = 0;  // modulo 2^32, like the reference's int32 sums of wrapped codes
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            q[r] = cvt_rne_x86(v[r] * inv);
+            usum += (uint32_t)q[r];
+        }
+        const int sum = (int)(usum + (uint32_t)dpp_i<DPP_XOR1>((int)usum));
+        uint4 c;
+        c.x = code_byte(q[0]) | (code_byte(q[1]) << 8) | (code_byte(q[2]) << 16) | (code_byte(q[3]) << 24);
+        c.y = code_byte(q[4]) | (code_byte(q[5]) << 8) | (code_byte(q[6]) << 16) | (code_byte(q[7]) << 24);
+        c.z = code_byte(q[8]) | (code_byte(q[9]) << 8) | (code_byte(q[10]) << 16) | (code_byte(q[11]) << 24);
+        c.w = code_byte(q[12]) | (code_byte(q[13]) << 8) | (code_byte(q[14]) << 16) | (code_byte(q[15]) << 24);
+        *reinterpret_cast<uint4*>(a.q + ((((int64_t)(t >> 5) * a.B + b) * 2 + h) * 32 + (t & 31)) * 16) = c;
+        if (h == 0) {
+            a.d[(int64_t)b * a.Tpad + t] = d;
+            a.cv[(int64_t)b * a.Tpad + t] = conversion_operand(sum);
+            a.ds[(int64_t)b * a.Tpad + t] = d * (float)sum;
+        }
+    }
 }
 
 hipError_t launch_rmsnorm_quant(const float* x, int ldx, const float* w, float eps, int n, const ActQ8& a,
                                 float* y_opt, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(a.Tpad), dim3(256), 2 * sizeof(float) * n, s, x, ldx, w, eps, n, a, y_opt);
+    if (n % 32 != 0) return hipErrorInvalidValue;
+    const size_t lds = sizeof(float) * ((size_t)n + 16 * (size_t)((((n >> 4) + 3) & ~3) + RMS_SQ_PAD));
+    hipLaunchKernelGGL(k_rmsnorm_quant, dim3(a.Tpad), dim3(256), lds, s, x, ldx, w, eps, n, a, y_opt);
     return hipGetLastError();
 }
 
