@@ -28,7 +28,7 @@ PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, TOP/s
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 TYPE_NAMES = {2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8: "Q8_0"}
-# The roofline is quoted for the GEMM kernel instantiation (k_gemm<type,TT,mode>, the name
+# The roofline is quoted for the GEMM kernel instantiation (k_gemm<type,TT,mode,BPS>, the name
 # rocprofv3 reports) with the most time in the timed region. HBM bytes per launch come
 # from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over that kernel, calibrated against a
 # device copy of known size, recorded in profiles/<kernel>_traffic.md.
@@ -472,16 +472,17 @@ def main():
 
     kernels = {}
     for t in TYPE_NAMES:
-        for tt in (1, 2, 4):
+        for tt in (1, 2):
             for mode in (0, 1, 2, 3):
-                name = f"k_gemm<{t},{tt},{mode}>"
-                c, cms, cops = model.profile_read(name)
-                if c:
-                    kernels[name] = (c, cms, cops)
+                for bps in (2, 4):
+                    name = f"k_gemm<{t},{tt},{mode},{bps}>"
+                    c, cms, cops = model.profile_read(name)
+                    if c:
+                        kernels[name] = (c, cms, cops)
     roof_kernel = max(kernels, key=lambda k: kernels[k][1])
     n, roof_ms, roof_ops = kernels[roof_kernel]
     achieved = roof_ops / (roof_ms * 1e-3) / 1e12 if roof_ms > 0 else 0.0
-    t_, tt_, mode_ = (int(v) for v in roof_kernel[7:-1].split(","))
+    t_, tt_, mode_, bps_ = (int(v) for v in roof_kernel[7:-1].split(","))
     breakdown = {}
     for cls in ["gemm*", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "attention", "k_attn_scores",
                 "k_attn_softmax", "k_attn_pv", "k_attn_fused", "rmsnorm_quant", "swiglu_quant", "quant_act", "rope_store", "embed",
@@ -525,7 +526,8 @@ def main():
                    "tokens": T, "weights": "Q4_0", "seed": args.seed},
         "roofline": {"bound": "mfma",
                      "kernel": f"{roof_kernel}: {TYPE_NAMES[t_]} block-quantized GEMM, {tt_} token tile(s) of 32 per "
-                               f"block, {EPILOGUES.get(mode_, 'store to the output')} (int8 ops vs the int8 peak)",
+                               f"block, {bps_} blocks per K-loop stage, {EPILOGUES.get(mode_, 'store to the output')} "
+                               f"(int8 ops vs the int8 peak)",
                      "achieved": round(achieved, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_INT8_TOPS, 4), "traffic": read_traffic(roof_kernel, T),
                      "ceiling": round(GEMM_CEILING_TOPS, 1),

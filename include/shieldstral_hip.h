@@ -200,7 +200,7 @@ shs_status shs_synchronize(shs_model* model);
  * bench times whole calls, Benchmark.cs:537-611). Classes by step: gemm_qkv, gemm_o,
  * gemm_gate_up, gemm_down, gemm_head, gemv, attention, rmsnorm_quant, swiglu_quant,
  * quant_act, rope_store, embed; and by kernel, under the names rocprofv3 reports:
- * "k_gemm<type,TT,mode>" (each GEMM launch is in both), k_attn_scores, k_attn_softmax,
+ * "k_gemm<type,TT,mode,BPS>" (each GEMM launch is in both), k_attn_scores, k_attn_softmax,
  * k_attn_pv, k_attn_fused. kernel_class "prefix*" sums the classes with that prefix.
  * total_ops is the algorithmic operation count (2·tokens·rows·cols for a GEMM), for
  * rmsnorm_quant the algorithmic HBM bytes (the rows read, their int8 codes and per-block

@@ -921,15 +921,17 @@ struct Capture {
 double gemm_ops(int T, const DevMatrix& w) { return 2.0 * T * (double)w.rows * w.cols; }
 
 // Each launch is timed under the projection's class and under its kernel instantiation,
-// "k_gemm<type,TT,mode>" (the name rocprofv3 reports, so the two can be compared).
+// "k_gemm<type,TT,mode,BPS>" (the name rocprofv3 reports, so the two can be compared).
 // The name rocprofv3 reports for the GEMM kernel launch_gemm* picks for this shape and mode.
 void gemm_kname(char* buf, size_t n, const DevMatrix& w, const ActQ8& a, int mode)
 {
     const int nt = gemm_narrow_tokens(w, a, mode);
     if (nt > 0)
         snprintf(buf, n, "k_gemm_narrow<%d,%d,%d>", w.type, nt, mode);
-    else
-        snprintf(buf, n, "k_gemm<%d,%d,%d>", w.type, gemm_token_tiles(w, a, mode), mode);
+    else {
+        const int tt = gemm_token_tiles(w, a, mode);
+        snprintf(buf, n, "k_gemm<%d,%d,%d,%d>", w.type, tt, mode, gemm_stage_blocks(w, tt));
+    }
 }
 
 shs_status run_proj(shs_model* m, const Proj& p, const ActQ8& a, float* y, int ldy, int mode, const char* cls)

@@ -133,6 +133,13 @@ hipError_t launch_gemm_qkv(const DevMatrix& w, const ActQ8& a, float* y, int ldy
                            const NormIn* norm = nullptr);
 // The token tiles per block launch_gemm picks for this shape (the k_gemm instantiation's TT).
 int gemm_token_tiles(const DevMatrix& w, const ActQ8& a, int mode);
+// Blocks per K-loop stage of that instantiation (its BPS): single-tile Q4_0 work-groups take
+// 4 when the block count is a multiple of 4 (three 16 KB slots, so three work-groups still
+// share a CU; the other types' larger slots would leave room for two), everything else 2.
+inline int gemm_stage_blocks(const DevMatrix& w, int token_tiles)
+{
+    return token_tiles == 1 && w.type == SHS_TYPE_Q4_0 && w.blocks % 4 == 0 ? 4 : 2;
+}
 // Up to NARROW_MAX_T tokens, launch_gemm, launch_gemm_qkv and launch_gemm_swiglu stream the
 // weights through k_gemm_narrow instead (same epilogues); returns the token count when they
 // do for this mode, else 0. With `with_norm`, whether the kernel can also form its input

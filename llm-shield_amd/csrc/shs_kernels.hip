@@ -802,33 +802,37 @@ typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 // scale step and the epilogue share the VALU's issue slots.
 // A work-group is 4 waves, one 32-row tile each, over TT 32-token tiles; the scale step pairs
 // the two token tiles (TT = 2) or two consecutive blocks (TT = 1). The K loop runs over stages
-// of two blocks through a ring of NS LDS slots filled by global → LDS copies NS − 1 stages
+// of BPS blocks through a ring of NS LDS slots filled by global → LDS copies NS − 1 stages
 // ahead, so memory latency hides behind NS − 1 stages of arithmetic; one barrier per stage.
+// Two-tile work-groups take stages of 2 blocks in 4 slots; single-tile work-groups, whose
+// slots are half as large, take stages of 4 blocks in 3 slots when the block count allows
+// (half the barriers and copy groups per block, the same LDS as 4 two-tile slots).
 // A slot holds the stage's activation codes and per-token operands (d_a, the conversion
 // column, d_a·Σq; shared by the 4 waves) and each wave's weight bytes and per-row factors
 // (d_w, fifth bits, m_w). D[i][j] (row i, token j) sits in lane j + 32·(i%8/4), register
 // 4·(i/8) + i%4.
-template <int TYPE, int TT>
+template <int TYPE, int TT, int BPS>
 struct GemmSlot {
+    static_assert((TT == 2 && BPS == 2) || (TT == 1 && (BPS == 2 || BPS == 4)), "stage shape");
     static constexpr bool OFF = (TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1);
     static constexpr bool QH = (TYPE == SHS_TYPE_Q5_0 || TYPE == SHS_TYPE_Q5_1);
     static constexpr bool Q8 = (TYPE == SHS_TYPE_Q8_0);
-    static constexpr int ACT = 2 * TT * 1024;  // [tile][block] 1 KB code chunks
-    // per-token operands: conversion columns [block][TT·32 tokens] 16 B, then d_a and d_a·Σq
-    // [block][TT·32 tokens] f32 (TT = 2: 2 KB + 1 KB; TT = 1: 1 KB + 1 KB incl. padding)
+    static constexpr int ACT = BPS * TT * 1024;  // [tile][block] 1 KB code chunks
     // per-token operands, [block][TT·32 tokens] each: conversion columns (8 B), then d_a and
-    // d_a·Σq (4 B) — TT copies of 1 KB
-    static constexpr int CV = 2 * TT * 32 * 8;
-    static constexpr int DA = 2 * TT * 32 * 4;
+    // d_a·Σq (4 B) — two copies of 1 KB (one of two masked halves at TT = 1, BPS = 2)
+    static constexpr int CV = BPS * TT * 32 * 8;
+    static constexpr int DA = BPS * TT * 32 * 4;
     static constexpr int FACT = CV + 2 * DA;
-    static constexpr int W = Q8 ? 2048 : 1024;               // per wave: [block][32 rows][QSB]
-    static constexpr int WX = 256 * (1 + QH + OFF);          // per wave: d_w [, qh] [, m_w], [block][32 rows]
+    static constexpr bool HALF_FACT = FACT == 1024;          // operand copies of half a wave each
+    static constexpr int W = (Q8 ? 1024 : 512) * BPS;        // per wave: [block][32 rows][QSB]
+    static constexpr int WX1 = 128 * BPS;                    // per wave and array: [block][32 rows] f32
+    static constexpr int WX = WX1 * (1 + QH + OFF);          // d_w [, qh] [, m_w]
     static constexpr int BYTES = ACT + FACT + 4 * (W + WX);
-    static constexpr int NSH_REAL = 2 * TT + 2;              // shared copies per stage: codes, then 2 of operands
-    static constexpr int SHARED = (NSH_REAL + 3) / 4;        // per wave (the last wave may repeat one)
-    static constexpr int OWN = (Q8 ? 2 : 1) + 1 + QH + OFF;  // each wave's own copies per stage
+    static constexpr int NSH_REAL = BPS * TT + 2;            // shared copies per stage: codes, then 2 of operands
+    static constexpr int SHARED = (NSH_REAL + 3) / 4;        // per wave (the last waves may repeat one)
+    static constexpr int OWN = W / 1024 + (1 + QH + OFF) * BPS / 2;  // each wave's own copies per stage
     static constexpr int PER_STAGE = SHARED + OWN;
-    static constexpr int NS = 4;                              // ring depth
+    static constexpr int NS = BPS == 4 ? 3 : 4;              // ring depth
 };
 
 // The down projection's input block (one 32-feature tile × token j) held as the MFMA D
@@ -866,13 +870,13 @@ __device__ __forceinline__ void quant_block_pair(const float* y, int h, const Ac
     }
 }
 
-template <int TYPE, int TT, int MODE>
+template <int TYPE, int TT, int MODE, int BPS>
 __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                  const float* __restrict__ wd, const float* __restrict__ wm,
                                                  int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N,
                                                  int n_tg, ActQ8 ao, int n_ft, RopeArgs ra)
 {
-    typedef GemmSlot<TYPE, TT> L;
+    typedef GemmSlot<TYPE, TT, BPS> L;
     constexpr bool OFF = L::OFF, QH = L::QH, Q8 = L::Q8;
     constexpr int NS = L::NS;
     constexpr int Z = ZeroPoint<TYPE>::z;
@@ -895,7 +899,8 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     const int rtl = active ? rt : ntiles - 1;  // inactive waves copy a valid tile (their share of the stage)
     const int ntt = a.Tpad >> 5;
     const int tt0 = tg * TT;
-    const int nstages = (B + 1) >> 1;
+    // (BPS = 4 is launched only for block counts that are a multiple of 4)
+    const int nstages = (B + BPS - 1) / BPS;
 
     // ---- the copy plan. Every copy of a stage is a scalar base that advances by a fixed
     // stride per stage plus a per-lane 32-bit offset fixed for the kernel, so issuing a stage
@@ -912,22 +917,23 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     for (int k = 0; k < L::SHARED; k++) {
         int i = wave + 4 * k;
         if (i >= L::NSH_REAL) i = 0;  // padding: repeat copy 0 (same bytes, same place)
-        if (i < 2 * TT) {
+        if (i < BPS * TT) {
             // activation codes of (tile u, block bb): 64 lanes × 16 B
-            const int u = i >> 1, bb = i & 1;
+            const int u = i / BPS, bb = i % BPS;
             const int tile = tt0 + u < ntt ? tt0 + u : ntt - 1;
             sh_base[k] = abase + ((int64_t)tile * B + bb) * 1024;
-            sh_stride[k] = 2048;
+            sh_stride[k] = BPS * 1024;
             sh_voff[k] = lane * 16;
             sh_lds[k] = i * 1024;
             sh_mask[k] = ~0ull;
         } else {
             // per-token operands, [block][TT·32 tokens] each in the slot: conversion columns
             // (8 B), d_a, d_a·Σq (4 B; d_a again when there is no offset term). Copy f = 0
-            // brings the columns, f = 1 the two float arrays; at TT = 2 each fills 64 lanes ×
-            // 16 B, at TT = 1 each fills one half of a 1 KB region (the other lanes masked off)
-            const int f = i - 2 * TT;
-            const int P = TT == 2 ? f * 1024 + lane * 16 : lane * 16;  // byte in the operand region
+            // brings the columns, f = 1 the two float arrays; each fills 64 lanes × 16 B, or,
+            // when the region is 1 KB (TT = 1, BPS = 2), one half of it (the other lanes
+            // masked off)
+            const int f = i - BPS * TT;
+            const int P = !L::HALF_FACT ? f * 1024 + lane * 16 : lane * 16;  // byte in the operand region
             int e;
             const uint8_t* arr;
             if (P < L::CV) {
@@ -942,10 +948,10 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
             int tok = e % (TT * 32);
             if ((tok >> 5) >= ntt - tt0) tok &= 31;  // a token tile past the end rereads tile tt0
             sh_base[k] = abase;
-            sh_stride[k] = 2 * ld * esize;
+            sh_stride[k] = BPS * ld * esize;
             sh_voff[k] = (uint32_t)(arr - abase) + (uint32_t)(((int64_t)bb * ld + tt0 * 32 + tok) * esize);
-            sh_lds[k] = 2 * TT * 1024 + (TT == 2 ? f * 1024 : 0);
-            sh_mask[k] = TT == 2 ? ~0ull : (f == 0 ? 0x00000000FFFFFFFFull : 0xFFFFFFFF00000000ull);
+            sh_lds[k] = BPS * TT * 1024 + (!L::HALF_FACT ? f * 1024 : 0);
+            sh_mask[k] = !L::HALF_FACT ? ~0ull : (f == 0 ? 0x00000000FFFFFFFFull : 0xFFFFFFFF00000000ull);
         }
     }
     const uint32_t w_voff = Q8 ? lane * 16 : h * 512 + j * 16;
@@ -957,81 +963,93 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
         const uint32_t slot_lds = ring_lds + slot * L::BYTES;
 #pragma unroll
         for (int k = 0; k < L::SHARED; k++) {
-            if (TT == 1)
+            if (L::HALF_FACT)
                 lds_copy16_s_masked(sh_base[k] + sidx * sh_stride[k], sh_voff[k], slot_lds + sh_lds[k], sh_mask[k]);
             else
                 lds_copy16_s(sh_base[k] + sidx * sh_stride[k], sh_voff[k], slot_lds + sh_lds[k]);
         }
-        // own copies: weight bytes of blocks 2s, 2s+1 and the per-row factors (d_w [, qh] [, m_w])
+        // own copies: weight bytes of the stage's BPS blocks and the per-row factors
+        // (d_w [, qh] [, m_w]), two blocks per copy (one for Q8_0's bytes)
         const uint32_t wlds = slot_lds + L::ACT + L::FACT + wave * L::W;
         const uint32_t xlds = slot_lds + L::ACT + L::FACT + 4 * L::W + wave * L::WX;
-        const int64_t rb = (int64_t)rtl * B + 2 * sidx;  // first block of the stage in the tile's records
+        const int64_t rb = (int64_t)rtl * B + BPS * sidx;  // first block of the stage in the tile's records
         if constexpr (Q8) {
-            lds_copy16_s(wqs + rb * 1024, w_voff, wlds);
-            lds_copy16_s(wqs + (rb + 1) * 1024, w_voff, wlds + 1024);
+#pragma unroll
+            for (int c = 0; c < BPS; c++) lds_copy16_s(wqs + (rb + c) * 1024, w_voff, wlds + c * 1024);
         } else {
-            lds_copy16_s(wqs + rb * 512, w_voff, wlds);
+#pragma unroll
+            for (int c = 0; c < BPS / 2; c++) lds_copy16_s(wqs + (rb + 2 * c) * 512, w_voff, wlds + c * 1024);
         }
-        lds_copy4_s(wd + rb * 32, x_voff, xlds);
-        if (QH) lds_copy4_s(wqh + rb * 32, x_voff, xlds + 256);
-        if (OFF) lds_copy4_s(wm + rb * 32, x_voff, xlds + 256 * (1 + QH));
+#pragma unroll
+        for (int c = 0; c < BPS / 2; c++) {
+            lds_copy4_s(wd + (rb + 2 * c) * 32, x_voff, xlds + c * 256);
+            if (QH) lds_copy4_s(wqh + (rb + 2 * c) * 32, x_voff, xlds + L::WX1 + c * 256);
+            if (OFF) lds_copy4_s(wm + (rb + 2 * c) * 32, x_voff, xlds + L::WX1 * (1 + QH) + c * 256);
+        }
     };
     // The last stage of an odd block count: its second block does not exist, and each copy
     // rereads block B−1 in its place (per-lane 64-bit addresses; runs once per kernel).
+    // (only two-block stages have one: four-block stages are launched for whole stages only)
     auto issue_last_odd = [&](int sidx, int slot) {
-        uint8_t* base = ring + slot * L::BYTES;
-        const int blk = B - 1;
-        // the lane index laundered here, so that nothing below is hoisted out of this rare
-        // path and kept live (in registers) across the K loop
-        int lane = threadIdx.x & 63;
-        asm volatile("" : "+v"(lane));
-        const int j = lane & 31;
-#pragma unroll
-        for (int k = 0; k < L::SHARED; k++) {
-            int i = wave + 4 * k;
-            if (i >= L::NSH_REAL) i = 0;
-            if (i < 2 * TT) {
-                const int u = i >> 1;
-                const int tile = tt0 + u < ntt ? tt0 + u : ntt - 1;
-                lds_copy16(a.q + ((int64_t)tile * B + blk) * 1024 + lane * 16, lds_addr(base + i * 1024));
-            } else {
-                const int f = i - 2 * TT;
-                const int P = TT == 2 ? f * 1024 + lane * 16 : lane * 16;
-                const bool mine = TT == 2 || (f == 0) == (lane < 32);
-                int e;
-                const uint8_t* arr;
-                if (P < L::CV) {
-                    e = P / 8, arr = reinterpret_cast<const uint8_t*>(a.cv);
-                } else if (P < L::CV + L::DA) {
-                    e = (P - L::CV) / 4, arr = reinterpret_cast<const uint8_t*>(a.d);
+        if constexpr (BPS == 2) {
+            uint8_t* base = ring + slot * L::BYTES;
+            const int blk = B - 1;
+            // the lane index laundered here, so that nothing below is hoisted out of this rare
+            // path and kept live (in registers) across the K loop
+            int lane = threadIdx.x & 63;
+            asm volatile("" : "+v"(lane));
+            const int j = lane & 31;
+    #pragma unroll
+            for (int k = 0; k < L::SHARED; k++) {
+                int i = wave + 4 * k;
+                if (i >= L::NSH_REAL) i = 0;
+                if (i < 2 * TT) {
+                    const int u = i >> 1;
+                    const int tile = tt0 + u < ntt ? tt0 + u : ntt - 1;
+                    lds_copy16(a.q + ((int64_t)tile * B + blk) * 1024 + lane * 16, lds_addr(base + i * 1024));
                 } else {
-                    e = (P - L::CV - L::DA) / 4, arr = reinterpret_cast<const uint8_t*>(OFF ? a.ds : a.d);
+                    const int f = i - 2 * TT;
+                    const int P = TT == 2 ? f * 1024 + lane * 16 : lane * 16;
+                    const bool mine = TT == 2 || (f == 0) == (lane < 32);
+                    int e;
+                    const uint8_t* arr;
+                    if (P < L::CV) {
+                        e = P / 8, arr = reinterpret_cast<const uint8_t*>(a.cv);
+                    } else if (P < L::CV + L::DA) {
+                        e = (P - L::CV) / 4, arr = reinterpret_cast<const uint8_t*>(a.d);
+                    } else {
+                        e = (P - L::CV - L::DA) / 4, arr = reinterpret_cast<const uint8_t*>(OFF ? a.ds : a.d);
+                    }
+                    const int esize = f == 0 ? 8 : 4;
+                    int tok = e % (TT * 32);
+                    if ((tok >> 5) >= ntt - tt0) tok &= 31;
+                    if (mine)
+                        lds_copy16(arr + ((int64_t)blk * ld + tt0 * 32 + tok) * esize,
+                                   lds_addr(base + 2 * TT * 1024 + (TT == 2 ? f * 1024 : 0)));
                 }
-                const int esize = f == 0 ? 8 : 4;
-                int tok = e % (TT * 32);
-                if ((tok >> 5) >= ntt - tt0) tok &= 31;
-                if (mine)
-                    lds_copy16(arr + ((int64_t)blk * ld + tt0 * 32 + tok) * esize,
-                               lds_addr(base + 2 * TT * 1024 + (TT == 2 ? f * 1024 : 0)));
             }
+            uint8_t* wbase = base + L::ACT + L::FACT + wave * L::W;
+            uint8_t* xbase = base + L::ACT + L::FACT + 4 * L::W + wave * L::WX;
+            if constexpr (Q8) {
+    #pragma unroll
+                for (int bb = 0; bb < 2; bb++)
+                    lds_copy16(wqs + ((int64_t)rtl * B + blk) * 1024 + lane * 16, lds_addr(wbase + bb * 1024));
+            } else {
+                lds_copy16(wqs + ((int64_t)rtl * B + blk) * 512 + j * 16, lds_addr(wbase));
+            }
+            const int64_t rec = ((int64_t)rtl * B + blk) * 32 + j;
+            lds_copy4(wd + rec, lds_addr(xbase));
+            if (QH) lds_copy4(wqh + rec, lds_addr(xbase + 256));
+            if (OFF) lds_copy4(wm + rec, lds_addr(xbase + 256 * (1 + QH)));
         }
-        uint8_t* wbase = base + L::ACT + L::FACT + wave * L::W;
-        uint8_t* xbase = base + L::ACT + L::FACT + 4 * L::W + wave * L::WX;
-        if constexpr (Q8) {
-#pragma unroll
-            for (int bb = 0; bb < 2; bb++)
-                lds_copy16(wqs + ((int64_t)rtl * B + blk) * 1024 + lane * 16, lds_addr(wbase + bb * 1024));
-        } else {
-            lds_copy16(wqs + ((int64_t)rtl * B + blk) * 512 + j * 16, lds_addr(wbase));
-        }
-        const int64_t rec = ((int64_t)rtl * B + blk) * 32 + j;
-        lds_copy4(wd + rec, lds_addr(xbase));
-        if (QH) lds_copy4(wqh + rec, lds_addr(xbase + 256));
-        if (OFF) lds_copy4(wm + rec, lds_addr(xbase + 256 * (1 + QH)));
     };
     auto issue = [&](int sidx, int slot) {
-        if (2 * sidx + 1 < B) issue_fast(sidx, slot);
-        else issue_last_odd(sidx, slot);
+        if constexpr (BPS == 4) {
+            issue_fast(sidx, slot);
+        } else {
+            if (2 * sidx + 1 < B) issue_fast(sidx, slot);
+            else issue_last_odd(sidx, slot);
+        }
     };
 
     v16f acc[TT];
@@ -1055,7 +1073,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
 
     // exact block sums of (token tile u, block bb) from the slot
     auto block_sums = [&](const uint8_t* base, v4i w, int u, int bb) -> v16f {
-        const v4i q = *reinterpret_cast<const v4i*>(base + (u * 2 + bb) * 1024 + h * 512 + j * 16);
+        const v4i q = *reinterpret_cast<const v4i*>(base + (u * BPS + bb) * 1024 + h * 512 + j * 16);
         const v16i F = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, q, magic, 0, 0, 0);
         const v4h c = *reinterpret_cast<const v4h*>(base + L::ACT + (bb * TT * 32 + u * 32 + j) * 8);
         return __builtin_amdgcn_mfma_f32_32x32x8f16(acv, c, __builtin_bit_cast(v16f, F), 0, 0, 0);
@@ -1067,7 +1085,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
         float dsv = dsa[bb * TT * 32 + u * 32 + j];
         dsv = valid ? dsv : 0.0f;
         const float4* m4p = reinterpret_cast<const float4*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX +
-                                                            256 * (1 + QH));
+                                                            L::WX1 * (1 + QH));
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const float4 m4 = m4p[bb * 8 + 2 * g + h];
@@ -1088,7 +1106,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
             const uint2 q = *reinterpret_cast<const uint2*>(wb + bb * 512 + j * 16 + h * 8);
             uint32_t qh = 0u;
             if (QH)
-                qh = reinterpret_cast<const uint32_t*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX + 256)[bb * 32 + j];
+                qh = reinterpret_cast<const uint32_t*>(base + L::ACT + L::FACT + 4 * L::W + wave * L::WX + L::WX1)[bb * 32 + j];
             return weights_i8<TYPE>(q.x, q.y, 0u, 0u, qh, h);
         }
     };
@@ -1097,17 +1115,17 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
     // Stage sidx lives in ring slot sidx % NS; the loop below runs whole rounds of the ring
     // with the slot a compile-time constant, so every LDS address is a fixed offset.
     // STEADY: a stage at least NS stages before the end, whose wait and copy issue need no
-    // checks (the stage it issues is never the odd last one).
+    // checks (the stage it issues is a whole one, never the odd last).
     auto stage = [&](int sidx, auto slot_c, auto steady_c) {
         constexpr int SLOT = decltype(slot_c)::value;
         if constexpr (decltype(steady_c)::value) {
-            wait_copies_barrier<2 * L::PER_STAGE>();
+            wait_copies_barrier<(NS - 2) * L::PER_STAGE>();
             issue_fast(sidx + NS - 1, (SLOT + NS - 1) % NS);
         } else {
             // stages issued after this one: NS − 2 in the steady state, fewer at the end
             const int ahead = nstages - 1 - sidx;
-            if (ahead >= 2) wait_copies_barrier<2 * L::PER_STAGE>();
-            else if (ahead == 1) wait_copies_barrier<L::PER_STAGE>();
+            if (ahead >= NS - 2) wait_copies_barrier<(NS - 2) * L::PER_STAGE>();
+            else if (NS == 4 && ahead == 1) wait_copies_barrier<L::PER_STAGE>();
             else wait_copies_barrier<0>();
             if (sidx + NS - 1 < nstages) issue(sidx + NS - 1, (SLOT + NS - 1) % NS);
         }
@@ -1118,7 +1136,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
         // A block past B (odd B, last stage) holds copies of block B−1: its d_w is taken as 0,
         // so S = 0 and fma(I, 0, acc) leaves acc unchanged (acc is never −0), and the loop body
         // needs no branch.
-        const bool valid1 = decltype(steady_c)::value || 2 * sidx + 1 < B;
+        const bool valid1 = BPS == 4 || decltype(steady_c)::value || 2 * sidx + 1 < B;
         if constexpr (TT == 2) {
 #pragma unroll
             for (int bb = 0; bb < 2; bb++) {
@@ -1142,46 +1160,67 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
                 }
             }
         } else {
-            const float da = da_s[h * 32 + j];
-            float dw = dw_s[h * 32 + j];
-            dw = (h == 0 || valid1) ? dw : 0.0f;
-            const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            const v16f G0 = block_sums(base, weights(base, 0), 0, 0);
-            const v16f G1 = block_sums(base, weights(base, 1), 0, 1);
+            // the scale step of blocks 2p and 2p + 1: lane half h holds block 2p + h
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G0[r], S[r], acc[0][r]);
-            if (OFF) offset_term(base, 0, 0, true);
+            for (int p = 0; p < BPS / 2; p++) {
+                const float da = da_s[(2 * p + h) * 32 + j];
+                float dw = dw_s[(2 * p + h) * 32 + j];
+                dw = (h == 0 || valid1) ? dw : 0.0f;
+                const v32f S = __builtin_amdgcn_mfma_f32_32x32x1f32(dw, da, zero32, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                const v16f G0 = block_sums(base, weights(base, 2 * p), 0, 2 * p);
+                const v16f G1 = block_sums(base, weights(base, 2 * p + 1), 0, 2 * p + 1);
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G1[r], S[16 + r], acc[0][r]);
-            if (OFF) offset_term(base, 1, 0, valid1);
+                for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G0[r], S[r], acc[0][r]);
+                if (OFF) offset_term(base, 2 * p, 0, true);
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[0][r] = fmaf(G1[r], S[16 + r], acc[0][r]);
+                if (OFF) offset_term(base, 2 * p + 1, 0, valid1);
+            }
         }
     };
-    static_assert(NS == 4, "the rounds below are written out for four slots");
     typedef std::integral_constant<int, 0> S0;
     typedef std::integral_constant<int, 1> S1;
     typedef std::integral_constant<int, 2> S2;
     typedef std::integral_constant<int, 3> S3;
     typedef std::true_type ST;
     typedef std::false_type CK;
+    // stages that hold BPS real blocks (all but an odd last one)
+    const int nfull = B / BPS;
     int sidx = 0;
-    // whole rounds whose every stage is steady (the round's last stage, sidx + 3, issues
-    // stage sidx + 6, which exists and is not the last), then the checked rounds
-    for (; sidx + 2 * NS - 1 <= nstages; sidx += NS) {
-        stage(sidx, S0(), ST());
-        stage(sidx + 1, S1(), ST());
-        stage(sidx + 2, S2(), ST());
-        stage(sidx + 3, S3(), ST());
+    // Whole rounds of the ring whose every stage is steady (the round's last stage issues
+    // stage sidx + 2·NS − 2, which must be a whole one), then the checked stages.
+    if constexpr (NS == 4) {
+        for (; sidx + 2 * NS - 1 <= nfull; sidx += NS) {
+            stage(sidx, S0(), ST());
+            stage(sidx + 1, S1(), ST());
+            stage(sidx + 2, S2(), ST());
+            stage(sidx + 3, S3(), ST());
+        }
+        for (; sidx + NS <= nstages; sidx += NS) {
+            stage(sidx, S0(), CK());
+            stage(sidx + 1, S1(), CK());
+            stage(sidx + 2, S2(), CK());
+            stage(sidx + 3, S3(), CK());
+        }
+        if (sidx < nstages) stage(sidx, S0(), CK());
+        if (sidx + 1 < nstages) stage(sidx + 1, S1(), CK());
+        if (sidx + 2 < nstages) stage(sidx + 2, S2(), CK());
+    } else {
+        static_assert(NS == 3, "rings of three or four slots");
+        for (; sidx + 2 * NS - 1 <= nfull; sidx += NS) {
+            stage(sidx, S0(), ST());
+            stage(sidx + 1, S1(), ST());
+            stage(sidx + 2, S2(), ST());
+        }
+        for (; sidx + NS <= nstages; sidx += NS) {
+            stage(sidx, S0(), CK());
+            stage(sidx + 1, S1(), CK());
+            stage(sidx + 2, S2(), CK());
+        }
+        if (sidx < nstages) stage(sidx, S0(), CK());
+        if (sidx + 1 < nstages) stage(sidx + 1, S1(), CK());
     }
-    for (; sidx + NS <= nstages; sidx += NS) {
-        stage(sidx, S0(), CK());
-        stage(sidx + 1, S1(), CK());
-        stage(sidx + 2, S2(), CK());
-        stage(sidx + 3, S3(), CK());
-    }
-    if (sidx < nstages) stage(sidx, S0(), CK());
-    if (sidx + 1 < nstages) stage(sidx + 1, S1(), CK());
-    if (sidx + 2 < nstages) stage(sidx + 2, S2(), CK());
     const int nv = ntt - tt0 < TT ? ntt - tt0 : TT;
     if constexpr (MODE == GEMM_SWIGLU) {
         // Exchange the accumulators through the (now idle) ring: X[wave][u][r][lane]; then
@@ -1296,14 +1335,21 @@ static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int 
     const int n_rg = MODE == GEMM_SWIGLU ? (n_ft + 1) / 2 : (w.tiles + 3) / 4;
     const int n_tg = ((a.Tpad >> 5) + TT - 1) / TT;
     dim3 grid((unsigned)(n_rg * n_tg)), block(256);
-    hipLaunchKernelGGL((k_gemm<TYPE, TT, MODE>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y, ldy,
-                       w.rows, n_tg, ao, n_ft, ra);
+    if constexpr (TYPE == SHS_TYPE_Q4_0 && TT == 1) {
+        if (gemm_stage_blocks(w, TT) == 4) {
+            hipLaunchKernelGGL((k_gemm<TYPE, 1, MODE, 4>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks,
+                               a, y, ldy, w.rows, n_tg, ao, n_ft, ra);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_gemm<TYPE, TT, MODE, 2>), grid, block, 0, s, w.qs, w.qh, w.d, w.m, w.tiles, w.blocks, a, y,
+                       ldy, w.rows, n_tg, ao, n_ft, ra);
     return hipGetLastError();
 }
 
-// Resident blocks of k_gemm<TYPE, TT, MODE> on the whole device (blocks per CU × CUs),
+// Resident blocks of k_gemm<TYPE, TT, MODE, BPS> on the whole device (blocks per CU × CUs),
 // asked of the runtime once per instantiation and device.
-template <int TYPE, int TT, int MODE>
+template <int TYPE, int TT, int MODE, int BPS>
 static int gemm_slots()
 {
     static int cached[64] = {0};
@@ -1311,7 +1357,7 @@ static int gemm_slots()
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
     if (cached[dev] == 0) {
         int per_cu = 0, n_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm<TYPE, TT, MODE>, 256, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm<TYPE, TT, MODE, BPS>, 256, 0) != hipSuccess ||
             hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
         cached[dev] = per_cu * n_cu;
@@ -1333,8 +1379,11 @@ static int gemm_tt_of(const DevMatrix& w, const ActQ8& a)
         return (double)blocks / (double)(rounds * slots);
     };
     if (ntt < 2) return 1;
-    const double f2 = fill(2, gemm_slots<TYPE, 2, MODE>());
-    if (f2 >= 0.9 || f2 >= fill(1, gemm_slots<TYPE, 1, MODE>())) return 2;
+    const double f2 = fill(2, gemm_slots<TYPE, 2, MODE, 2>());
+    int slots1 = 0;
+    if constexpr (TYPE == SHS_TYPE_Q4_0) slots1 = gemm_stage_blocks(w, 1) == 4 ? gemm_slots<TYPE, 1, MODE, 4>() : 0;
+    if (slots1 == 0) slots1 = gemm_slots<TYPE, 1, MODE, 2>();
+    if (f2 >= 0.9 || f2 >= fill(1, slots1)) return 2;
     return 1;
 }
 
