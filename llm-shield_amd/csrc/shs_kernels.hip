@@ -2555,7 +2555,9 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
 // 32 row maxima. Blocks map to (KV-head group, head in group) so that the group's heads —
 // which read the same K and V rows — share an XCD and start together: block b runs group
 // 8·(b >> 5) + (b & 7) (groups longest first) and head (b >> 3) & 3 of it.
-constexpr int ATT_RMAX = 4 * 32;  // floats of the row maxima after the score tiles
+constexpr int ATT_THREADS = 512;  // eight waves: two per SIMD in the score and softmax phases
+constexpr int ATT_RMAX = (ATT_THREADS / 64) * 32;  // floats of the row maxima after the score tiles
+constexpr int ATT_QLDS = 32 * ATT_HD;              // floats of the query rows after the maxima and Σe
 
 __device__ __forceinline__ int att_swz(int j, int t) { return j * 32 + ((t ^ (j & 7)) << 2); }
 
@@ -2570,8 +2572,9 @@ __device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc,
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, h = lane >> 5;
+    const bool vwave = wave < ATT_HD / 32;  // waves 0..3 each run one 32-dimension slice
     const float* vbase = vc + ((int64_t)kvh * cap + it.key_start) * ATT_HD;
-    const int voff = h * (ATT_HD * 4) + (32 * wave + j) * 4;  // bytes
+    const int voff = h * (ATT_HD * 4) + (32 * (wave & 3) + j) * 4;  // bytes
     struct VOps {
         float a[16];  // V of key 2c + h, dimension 32·wave + j
     };
@@ -2608,9 +2611,12 @@ __device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc,
     for (int r = 0; r < 16; r++) o[r] = 0.0f;
     VOps va, vb;
     WOps wa, wb;
-    vload(0, va);
-    vload(1, vb);
+    if (vwave) {
+        vload(0, va);
+        vload(1, vb);
+    }
     __syncthreads();  // every w is written
+    if (!vwave) return;
     wread(0, wa);
     // iteration kt: `cur` holds V(kt) (V(kt + 1) in flight), `w` tile kt's weights; it reads
     // tile kt + 1's weights, issues tile kt's 16 MFMAs, then loads V(kt + 2) into `cur`
@@ -2647,15 +2653,18 @@ __device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc,
         *reinterpret_cast<float4*>(outp + 8 * gq + 4 * h) = make_float4(o[4 * gq], o[4 * gq + 1], o[4 * gq + 2], o[4 * gq + 3]);
 }
 
-__global__ __launch_bounds__(256, 1) void k_attn_fused(const float* __restrict__ q, int ldq,
-                                                      const float* __restrict__ kc, const float* __restrict__ vc,
-                                                      int cap, const AttnItem* __restrict__ items, int n_items,
-                                                      int n_head, int n_kv, float scale, float* __restrict__ ctx,
-                                                      int ldc, ActQ8 ao, int kt_cap)
+__global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __restrict__ q, int ldq,
+                                                              const float* __restrict__ kc,
+                                                              const float* __restrict__ vc, int cap,
+                                                              const AttnItem* __restrict__ items, int n_items,
+                                                              int n_head, int n_kv, float scale,
+                                                              float* __restrict__ ctx, int ldc, ActQ8 ao, int kt_cap)
 {
     extern __shared__ float4 att_lds4[];
     float* S = reinterpret_cast<float*>(att_lds4);
     float* rmax = S + (int64_t)kt_cap * 1024;  // [wave][query row] maxima of the score phase
+    float* tot = rmax + ATT_RMAX;               // [query row] Σe
+    float* qlds = tot + 32;                     // [step][half][query][8] query operands
     const int tid = threadIdx.x;
     const int b = blockIdx.x;
     const int g = 8 * (b >> 5) + (b & 7), hg = (b >> 3) & 3;
@@ -2677,16 +2686,16 @@ __global__ __launch_bounds__(256, 1) void k_attn_fused(const float* __restrict__
         // A operands: row i of the A tile carries key kap(i), so D row i holds key kap(i),
         // and register r of lane half h holds key 2r + h
         const int kap = 8 * (j >> 3) + 2 * (j & 3) + ((j >> 2) & 1);
-        // B operands: step s of chain l needs q[l + 16s + 8h]; qv[s] holds l = 0..7
-        v4f qv[8][2];
-        {
-            const float* qrow = q + (int64_t)(it.q_start + (q_ok ? j : 0)) * ldq + head * ATT_HD + 8 * h;
-#pragma unroll
-            for (int s = 0; s < 8; s++)
-#pragma unroll
-                for (int x = 0; x < 2; x++)
-                    qv[s][x] = q_ok ? *reinterpret_cast<const v4f*>(qrow + 16 * s + 4 * x) : v4f{0.f, 0.f, 0.f, 0.f};
+        // B operands: step s of chain l needs q[l + 16s + 8h], l = 0..7 — the block's 32
+        // query rows go to the LDS once, as [s][h][query][l] (zeros past the item's queries)
+        for (int f = tid; f < 32 * ATT_HD / 4; f += ATT_THREADS) {
+            const int jq = f >> 5, d0 = (f & 31) * 4;
+            v4f v = {0.f, 0.f, 0.f, 0.f};
+            if (jq < it.q_count)
+                v = *reinterpret_cast<const v4f*>(q + (int64_t)(it.q_start + jq) * ldq + head * ATT_HD + d0);
+            *reinterpret_cast<v4f*>(qlds + (((d0 >> 4) * 2 + ((d0 >> 3) & 1)) * 32 + jq) * 8 + (d0 & 7)) = v;
         }
+        const v4f* qop = reinterpret_cast<const v4f*>(qlds + (h * 32 + j) * 8);  // step s at qop[s * 128]
         // K operands of step s of tile kt: k[l + 16s + 8h] of key kap, l = 0..7; rows past
         // the item's last key read that key (their scores are masked)
         auto kload = [&](int kt, int s, v4f (&k)[2]) {
@@ -2694,8 +2703,9 @@ __global__ __launch_bounds__(256, 1) void k_attn_fused(const float* __restrict__
             k[0] = *reinterpret_cast<const v4f*>(src);
             k[1] = *reinterpret_cast<const v4f*>(src + 4);
         };
-        const int n_mine = n_kt > wave ? (n_kt - wave + 3) >> 2 : 0;  // tiles wave, wave + 4, ...
-        const int last = wave + 4 * (n_mine > 0 ? n_mine - 1 : 0);
+        constexpr int NW = ATT_THREADS / 64;
+        const int n_mine = n_kt > wave ? (n_kt - wave + NW - 1) / NW : 0;  // tiles wave, wave + NW, ...
+        const int last = wave + NW * (n_mine > 0 ? n_mine - 1 : 0);
         float mx = -INFINITY;
         v4f kr[4][2];  // ring: step g of the wave's step sequence in slot g & 3, loaded 3 steps ahead
         if (n_mine > 0) {
@@ -2703,27 +2713,29 @@ __global__ __launch_bounds__(256, 1) void k_attn_fused(const float* __restrict__
             kload(wave, 1, kr[1]);
             kload(wave, 2, kr[2]);
         }
+        __syncthreads();  // the query operands are in the LDS
         for (int u = 0; u < n_mine; u++) {
-            const int kt = wave + 4 * u;
-            const int ktn = min(kt + 4, last);  // the wave's next tile; its last tile repeats
+            const int kt = wave + NW * u;
+            const int ktn = min(kt + NW, last);  // the wave's next tile; its last tile repeats
             v16f c[8];
 #pragma unroll
             for (int s = 0; s < 8; s++) {
                 if (s < 5) kload(kt, s + 3, kr[(s + 3) & 3]);
                 else kload(ktn, s - 5, kr[(s + 3) & 3]);
+                const v4f q0 = qop[s * 128], q1 = qop[s * 128 + 1];
                 // the loads go out before this step's MFMAs
                 __builtin_amdgcn_sched_barrier(0);
                 const v4f k0 = kr[s & 3][0], k1 = kr[s & 3][1];
                 const v16f z = {};
                 // the 8 chains advance together: step s is 8 independent MFMAs
-                c[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.x, qv[s][0].x, s ? c[0] : z, 0, 0, 0);
-                c[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.y, qv[s][0].y, s ? c[1] : z, 0, 0, 0);
-                c[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.z, qv[s][0].z, s ? c[2] : z, 0, 0, 0);
-                c[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.w, qv[s][0].w, s ? c[3] : z, 0, 0, 0);
-                c[4] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.x, qv[s][1].x, s ? c[4] : z, 0, 0, 0);
-                c[5] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.y, qv[s][1].y, s ? c[5] : z, 0, 0, 0);
-                c[6] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.z, qv[s][1].z, s ? c[6] : z, 0, 0, 0);
-                c[7] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.w, qv[s][1].w, s ? c[7] : z, 0, 0, 0);
+                c[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.x, q0.x, s ? c[0] : z, 0, 0, 0);
+                c[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.y, q0.y, s ? c[1] : z, 0, 0, 0);
+                c[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.z, q0.z, s ? c[2] : z, 0, 0, 0);
+                c[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.w, q0.w, s ? c[3] : z, 0, 0, 0);
+                c[4] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.x, q1.x, s ? c[4] : z, 0, 0, 0);
+                c[5] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.y, q1.y, s ? c[5] : z, 0, 0, 0);
+                c[6] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.z, q1.z, s ? c[6] : z, 0, 0, 0);
+                c[7] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.w, q1.w, s ? c[7] : z, 0, 0, 0);
             }
             float sc[16];
 #pragma unroll
@@ -2757,63 +2769,89 @@ __global__ __launch_bounds__(256, 1) void k_attn_fused(const float* __restrict__
         __syncthreads();  // every score and maximum is written
     }
 
-    // ---- softmax: e in place, Σe, then w = e / Σe in place
+    // ---- softmax: thread (p, j, t) owns residue t of query row j in half p of the tiles.
+    // Both halves form e in place; then half 0 forms Σe in Kernels.Softmax's order over every
+    // tile; then both halves form w = e / Σe in place.
     {
-        const int j = tid >> 3, t = tid & 7;
+        const int p = tid >> 8, r = tid & 255;
+        const int j = r >> 3, t = r & 7;
         const bool qvalid = j < it.q_count;
         const int nq = it.pos0 + j + 1;
         const int n8 = nq & ~7;
-        const float mx = __builtin_elementwise_maximum(__builtin_elementwise_maximum(rmax[j], rmax[32 + j]),
-                                                       __builtin_elementwise_maximum(rmax[64 + j], rmax[96 + j]));
+        float mx = rmax[j];
+#pragma unroll
+        for (int w = 1; w < ATT_THREADS / 64; w++) mx = __builtin_elementwise_maximum(mx, rmax[w * 32 + j]);
         const bool nan = mx != mx;
         const bool uniform = nan || !(fabsf(mx) <= 3.402823466e38f);
         const int sw = att_swz(j, t);
-        float lane_sum = 0.0f, tail_e = 0.0f;
         const int full_kt = ((it.pos0 + 1) & ~7) >> 5;
         const bool fast = !__any(qvalid && uniform);
+        const int kh = (n_kt + 1) >> 1;  // tiles [0, kh) in half 0, [kh, n_kt) in half 1
+        const int k0 = p ? kh : 0, k1 = p ? n_kt : kh;
         constexpr int NB = 4;
-        for (int kt0 = 0; kt0 < n_kt; kt0 += NB) {
+        for (int kt0 = k0; kt0 < k1; kt0 += NB) {
             float4 sv[NB];
 #pragma unroll
             for (int qq = 0; qq < NB; qq++)
-                sv[qq] = *reinterpret_cast<const float4*>(S + (kt0 + qq < n_kt ? kt0 + qq : kt0) * 1024 + sw);
+                sv[qq] = *reinterpret_cast<const float4*>(S + (kt0 + qq < k1 ? kt0 + qq : kt0) * 1024 + sw);
 #pragma unroll
             for (int qq = 0; qq < NB; qq++) {
-                if (kt0 + qq >= n_kt) break;
+                if (kt0 + qq >= k1) break;
                 const float sc[4] = {sv[qq].x, sv[qq].y, sv[qq].z, sv[qq].w};
                 float e[4];
                 if (fast && kt0 + qq < full_kt) {
 #pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        e[k] = det_expf_nonpos(sc[k] - mx);
-                        lane_sum = lane_sum + e[k];
-                    }
+                    for (int k = 0; k < 4; k++) e[k] = det_expf_nonpos(sc[k] - mx);
                 } else {
 #pragma unroll
                     for (int k = 0; k < 4; k++) {
                         const int key = (kt0 + qq) * 32 + t + 8 * k;
                         const float ex = uniform ? 1.0f : det_expf(sc[k] - mx);
                         e[k] = qvalid && key < nq ? ex : 0.0f;
-                        lane_sum = key < n8 ? lane_sum + e[k] : lane_sum;
-                        tail_e = key >= n8 && key < nq ? e[k] : tail_e;
                     }
                 }
                 *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
             }
         }
-        float total = vsum8_lanes(lane_sum);
+        __syncthreads();  // every e is written
+        if (p == 0) {
+            // Σe: lane t sums its residue's keys below n8 in key order, the 8 lanes pairwise,
+            // then the keys n8 .. nq − 1 in order
+            float lane_sum = 0.0f, tail_e = 0.0f;
+            for (int kt0 = 0; kt0 < n_kt; kt0 += NB) {
+                float4 ev[NB];
 #pragma unroll
-        for (int k = 0; k < 7; k++) {
-            const float e = __shfl(tail_e, k, 8);
-            if (n8 + k < nq) total = total + e;
+                for (int qq = 0; qq < NB; qq++)
+                    ev[qq] = *reinterpret_cast<const float4*>(S + (kt0 + qq < n_kt ? kt0 + qq : kt0) * 1024 + sw);
+#pragma unroll
+                for (int qq = 0; qq < NB; qq++) {
+                    if (kt0 + qq >= n_kt) break;
+                    const float e[4] = {ev[qq].x, ev[qq].y, ev[qq].z, ev[qq].w};
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        const int key = (kt0 + qq) * 32 + t + 8 * k;
+                        lane_sum = key < n8 ? lane_sum + e[k] : lane_sum;
+                        tail_e = key >= n8 && key < nq ? e[k] : tail_e;
+                    }
+                }
+            }
+            float total = vsum8_lanes(lane_sum);
+#pragma unroll
+            for (int k = 0; k < 7; k++) {
+                const float e = __shfl(tail_e, k, 8);
+                if (n8 + k < nq) total = total + e;
+            }
+            if (t == 0) tot[j] = total;
         }
+        __syncthreads();  // every Σe is written
         if (qvalid) {
+            const float total = tot[j];
             const float rcp = 1.0f / total;
-            for (int kt0 = 0; kt0 < n_kt; kt0 += 4) {
+            for (int kt0 = k0; kt0 < k1; kt0 += 4) {
                 float e[16], w[16];
 #pragma unroll
                 for (int qq = 0; qq < 4; qq++) {
-                    const int kt = kt0 + qq < n_kt ? kt0 + qq : kt0;  // past the end: reread, not written
+                    const int kt = kt0 + qq < k1 ? kt0 + qq : kt0;  // past the end: reread, not written
                     const float4 v = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
                     e[4 * qq] = v.x;
                     e[4 * qq + 1] = v.y;
@@ -2823,7 +2861,7 @@ __global__ __launch_bounds__(256, 1) void k_attn_fused(const float* __restrict__
                 softmax_divide<16>(e, w, total, rcp);
 #pragma unroll
                 for (int qq = 0; qq < 4; qq++)
-                    if (kt0 + qq < n_kt)
+                    if (kt0 + qq < k1)
                         *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) =
                             make_float4(w[4 * qq], w[4 * qq + 1], w[4 * qq + 2], w[4 * qq + 3]);
             }
@@ -2934,7 +2972,7 @@ hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n
 
 int attn_fused_kt_limit(int max_lds_bytes)
 {
-    const int kt = (max_lds_bytes - ATT_RMAX * (int)sizeof(float)) / (1024 * (int)sizeof(float));
+    const int kt = (max_lds_bytes - (ATT_RMAX + 32 + ATT_QLDS) * (int)sizeof(float)) / (1024 * (int)sizeof(float));
     return kt > 0 ? kt : 0;
 }
 
@@ -2946,7 +2984,7 @@ hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const flo
     if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4 || kt_cap <= 0) return hipErrorInvalidValue;
     if (codes && (codes->B != n_head * ATT_HD / 32 || !codes->q)) return hipErrorInvalidValue;
     const ActQ8 ao = codes ? *codes : ActQ8();
-    const size_t lds = ((size_t)kt_cap * 1024 + ATT_RMAX) * sizeof(float);
+    const size_t lds = ((size_t)kt_cap * 1024 + ATT_RMAX + 32 + ATT_QLDS) * sizeof(float);
     static int attr_set = 0;
     if (attr_set < (int)lds) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_fused),
@@ -2956,7 +2994,7 @@ hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const flo
     }
     const int n_groups = n_items * n_kv;
     const unsigned grid = (unsigned)(((n_groups + 7) / 8) * 32);
-    hipLaunchKernelGGL(k_attn_fused, dim3(grid), dim3(256), lds, s, q, ldq, kc, vc, cap, items, n_items, n_head, n_kv,
+    hipLaunchKernelGGL(k_attn_fused, dim3(grid), dim3(ATT_THREADS), lds, s, q, ldq, kc, vc, cap, items, n_items, n_head, n_kv,
                        scale, ctx, ldc, ao, kt_cap);
     return hipGetLastError();
 }

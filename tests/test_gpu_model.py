@@ -52,15 +52,16 @@ def test_forward_matches_oracle_and_first_layer_is_bit_exact(shs, oracle, tiny):
 
 def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
     """A pass whose longest 32-query item has at most as many key tiles as one block's LDS
-    holds (39 tiles of 32 keys in 160 KB) runs scores, softmax and values in one kernel
-    (k_attn_fused); a longer one (here 1300 keys) takes the three-kernel path. Both are
-    bit-exact, including a pass that starts mid-tile and one at the fused kernel's limit
-    (1240 keys: 39 tiles, the last partial)."""
+    holds (35 tiles of 32 keys beside the row maxima, the row sums and the 16 KB of query
+    rows in 160 KB) runs scores, softmax and values in one kernel (k_attn_fused); a longer
+    one (here 1300 keys) takes the three-kernel path. Both are bit-exact, including a pass
+    that starts mid-tile and one at the fused kernel's limit (1110 keys: 35 tiles, the last
+    partial)."""
     cfg, tensors, types, gpu, ora = tiny
     long_ora = oracle.OracleModel(cfg, tensors, types, cap=1400)
     rng = np.random.default_rng(11)
     ids = [1, 200, 511]
-    for prefix, n, fused in ((0, 70, True), (45, 50, True), (0, 1240, True), (0, 1300, False)):
+    for prefix, n, fused in ((0, 70, True), (45, 50, True), (0, 1110, True), (0, 1300, False)):
         toks = rng.integers(0, cfg.vocab, prefix + n)
         gpu.reset_kv_cache()
         long_ora.reset()
