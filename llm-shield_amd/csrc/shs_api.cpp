@@ -368,11 +368,13 @@ struct shs_model {
     int n_cu = 0;          // compute units of the device (persistent kernel sizing)
     int fused_kt = 0;      // most key tiles an item may have for the fused softmax + values kernel
     int max_kt = 0;        // key tiles of the longest placed item
+    int max_kt_fused = 0;  // key tiles of the longest item the fused kernel takes
+    int n_long = 0;        // placed items past fused_kt key tiles: the first n_long of the list
     int max_lds = 0;       // LDS bytes a block may use (opt-in)
     int max_qc = 0;        // queries of the widest placed item
     int max_keys = 0;      // keys of the longest placed item
     int64_t score_floats = 0, pm_floats = 0;
-    int64_t attn_pairs = 0;
+    int64_t attn_pairs = 0, attn_pairs_long = 0;
     ActBuf act;
     ActBuf act_ffn;  // the fused gate|up GEMM's output codes (its input codes live in act)
     HostBuf stage;   // pinned staging of a call's small uploads (upload())
@@ -1093,6 +1095,7 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
             int* ctr = m->counters.as<int>();
             // 2·head_dim flops per (query, key) pair and head, for the scores and again for the values
             const double attn_ops = 2.0 * c.head_dim * c.n_head * (double)m->attn_pairs;
+            const double long_ops = 2.0 * c.head_dim * c.n_head * (double)m->attn_pairs_long;
             if (m->max_qc <= ATT_DEC_MAX_Q && c.n_head / c.n_kv_head <= 4 &&
                 m->max_keys <= attn_decode_max_keys(m->max_qc, m->max_lds)) {
                 // decode width: scores per (KV head, 64-key chunk), values per (head, 32-dim slice)
@@ -1100,29 +1103,35 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
                 HIP_TRY(launch_attn_decode(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head,
                                            c.head_dim, scale, m->max_qc, m->max_keys, scr, ctx, qdim,
                                            cap_on ? nullptr : &ac, m->stream));
-            } else if (m->max_kt <= m->fused_kt) {
-                // every item's scores fit one block's LDS: scores, softmax and values in one
-                // kernel; without capture it writes the o projection's activation codes itself
-                Timed tk(m->prof, "k_attn_fused", 2 * attn_ops, m->stream, "attention");
-                HIP_TRY(launch_attn_fused(qkv, ldqkv, kc, vc, cap, items_dev, n_items, c.n_head, c.n_kv_head,
-                                          c.head_dim, scale, ctx, qdim, cap_on ? nullptr : &ac, m->max_kt, m->stream));
             } else {
-                {
-                    Timed tk(m->prof, "k_attn_scores", attn_ops, m->stream, "attention");
-                    HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(), m->n_chunks,
-                                               c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm, m->stream));
-                }
-                {
+                // Items past the fused kernel's key tiles (the first n_long of the list) take the
+                // three kernels through the score scratch; the rest the fused kernel, whose block
+                // holds an item's scores in its LDS and which, without capture, writes the o
+                // projection's activation codes itself. The two sets of items write disjoint rows.
+                const int n_long = m->n_long, n_fused = n_items - n_long;
+                if (n_long > 0) {
+                    {
+                        Timed tk(m->prof, "k_attn_scores", long_ops, m->stream, "attention");
+                        HIP_TRY(launch_attn_scores(qkv, ldqkv, kc, cap, items_dev, m->chunks.as<AttnChunk>(),
+                                                   m->n_chunks, c.n_head, c.n_kv_head, c.head_dim, scale, scr, pm,
+                                                   m->stream));
+                    }
                     {
                         Timed tk(m->prof, "k_attn_softmax", 0, m->stream, "attention");
-                        HIP_TRY(launch_attn_softmax(items_dev, n_items, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu,
+                        HIP_TRY(launch_attn_softmax(items_dev, n_long, c.n_head, c.n_kv_head, scr, pm, ctr, m->n_cu,
                                                     m->stream));
                     }
                     {
-                        Timed tk(m->prof, "k_attn_pv", attn_ops, m->stream, "attention");
-                        HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_items, c.n_head, c.n_kv_head, scr, ctx, qdim,
+                        Timed tk(m->prof, "k_attn_pv", long_ops, m->stream, "attention");
+                        HIP_TRY(launch_attn_pv(vc, cap, items_dev, n_long, c.n_head, c.n_kv_head, scr, ctx, qdim,
                                                cap_on ? nullptr : &ac, ctr, m->n_cu, m->stream));
                     }
+                }
+                if (n_fused > 0) {
+                    Timed tk(m->prof, "k_attn_fused", 2 * (attn_ops - long_ops), m->stream, "attention");
+                    HIP_TRY(launch_attn_fused(qkv, ldqkv, kc, vc, cap, items_dev + n_long, n_fused, c.n_head,
+                                              c.n_kv_head, c.head_dim, scale, ctx, qdim, cap_on ? nullptr : &ac,
+                                              m->max_kt_fused, m->stream));
                 }
             }
         }
@@ -1260,22 +1269,31 @@ hipError_t upload(shs_model* m, void* dst, const void* src, size_t bytes)
     return e != hipSuccess ? e : hipStreamSynchronize(m->stream);
 }
 
-// Gives every item its own region of the score scratch (4 waves per KV head, one 32×32
-// tile of 1024 floats per key tile), splits the items' key tiles into the score kernel's
-// chunks (longest items first, so they start first) and sizes the scratch: score tiles,
-// then 32 row maxima per tile.
+// Orders the items for the attention kernels: those past the fused kernel's key tiles first,
+// then those it takes, each group by ascending length (the kernels start from the end of
+// their group, longest first). Gives every item its own region of the score scratch (4 waves
+// per KV head, one 32×32 tile of 1024 floats per key tile), splits the long items' key tiles
+// into the score kernel's chunks and sizes the scratch: score tiles, then 32 row maxima per
+// tile.
 // The chunk length c (2..8 key tiles) minimizes rounds × (c + 1): the score kernel's blocks
 // fill its resident slots round by round, and a block costs about one tile more than its
 // tiles for its own start (the q and first K loads). Ties go to the shorter chunk.
 shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
 {
+    auto tiles = [](const AttnItem& it) { return (it.pos0 + it.q_count + 31) / 32; };
+    std::stable_sort(items.begin(), items.end(),
+                     [&](const AttnItem& a, const AttnItem& b) { return tiles(a) < tiles(b); });
+    const int fused_kt = m->fused_kt;
+    std::stable_partition(items.begin(), items.end(), [&](const AttnItem& it) { return tiles(it) > fused_kt; });
+    int n_long = 0;
+    while (n_long < (int)items.size() && tiles(items[n_long]) > fused_kt) n_long++;
     int kChunk = 4;
     {
         const int64_t slots = std::max(1, attn_score_slots(m->n_cu));
         int64_t best = -1;
         for (int c = 2; c <= 8; c++) {
             int64_t blocks = 0;
-            for (const auto& it : items) blocks += ((it.pos0 + it.q_count + 31) / 32 + c - 1) / c;
+            for (int i = 0; i < n_long; i++) blocks += (tiles(items[i]) + c - 1) / c;
             blocks *= m->cfg.n_kv_head;
             const int64_t cost = (blocks + slots - 1) / slots * (c + 1);
             if (best < 0 || cost < best) {
@@ -1284,27 +1302,36 @@ shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
             }
         }
     }
+    // every item gets a region: the decode-width kernels keep their scores there too
     int64_t off = 0;
     for (auto& it : items) {
         it.s_off = off;
-        int64_t n_kt = (it.pos0 + it.q_count + 31) / 32;
-        off += n_kt * 1024 * (int64_t)m->cfg.n_kv_head * 4;
+        off += (int64_t)tiles(it) * 1024 * (int64_t)m->cfg.n_kv_head * 4;
     }
     std::vector<AttnChunk> chunks;
-    for (int i = (int)items.size() - 1; i >= 0; i--) {
-        const int n_kt = (items[i].pos0 + items[i].q_count + 31) / 32;
+    for (int i = n_long - 1; i >= 0; i--) {
+        const int n_kt = tiles(items[i]);
         for (int k = 0; k < n_kt; k += kChunk) chunks.push_back({i, k, std::min(kChunk, n_kt - k), 0});
     }
     m->score_floats = off;
     m->pm_floats = off / 32;
-    m->max_kt = m->max_qc = m->max_keys = 0;
-    for (const auto& it : items) {
-        m->max_kt = std::max(m->max_kt, (it.pos0 + it.q_count + 31) / 32);
+    m->n_long = n_long;
+    m->max_kt = m->max_kt_fused = m->max_qc = m->max_keys = 0;
+    for (int i = 0; i < (int)items.size(); i++) {
+        const auto& it = items[i];
+        m->max_kt = std::max(m->max_kt, tiles(it));
+        if (i >= n_long) m->max_kt_fused = std::max(m->max_kt_fused, tiles(it));
         m->max_qc = std::max(m->max_qc, it.q_count);
         m->max_keys = std::max(m->max_keys, it.pos0 + it.q_count);
     }
-    m->attn_pairs = 0;  // (query, key) pairs the items attend over
-    for (const auto& it : items) m->attn_pairs += (int64_t)it.q_count * it.pos0 + (int64_t)it.q_count * (it.q_count + 1) / 2;
+    // (query, key) pairs the items attend over, and those of the long items
+    m->attn_pairs = m->attn_pairs_long = 0;
+    for (int i = 0; i < (int)items.size(); i++) {
+        const auto& it = items[i];
+        const int64_t pairs = (int64_t)it.q_count * it.pos0 + (int64_t)it.q_count * (it.q_count + 1) / 2;
+        m->attn_pairs += pairs;
+        if (i < n_long) m->attn_pairs_long += pairs;
+    }
     HIP_TRY(m->scores.ensure(sizeof(float) * (size_t)std::max<int64_t>(off + m->pm_floats, 1)));
     HIP_TRY(m->items.ensure(sizeof(AttnItem) * items.size()));
     HIP_TRY(upload(m, m->items.p, items.data(), sizeof(AttnItem) * items.size()));

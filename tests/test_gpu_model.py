@@ -51,12 +51,13 @@ def test_forward_matches_oracle_and_first_layer_is_bit_exact(shs, oracle, tiny):
 
 
 def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
-    """A pass whose longest 32-query item has at most as many key tiles as one block's LDS
-    holds (35 tiles of 32 keys beside the row maxima, the row sums and the 16 KB of query
-    rows in 160 KB) runs scores, softmax and values in one kernel (k_attn_fused); a longer
-    one (here 1300 keys) takes the three-kernel path. Both are bit-exact, including a pass
-    that starts mid-tile and one at the fused kernel's limit (1110 keys: 35 tiles, the last
-    partial)."""
+    """A 32-query item with at most as many key tiles as one block's LDS holds (35 tiles of
+    32 keys beside the row maxima, the row sums and the 16 KB of query rows in 160 KB) runs
+    scores, softmax and values in one kernel (k_attn_fused); a longer one takes the
+    three-kernel path. A pass of 1300 keys runs both in each layer: its last items (keys
+    past 1120) through the three kernels, the rest through the fused one. All bit-exact,
+    including a pass that starts mid-tile and one at the fused kernel's limit (1110 keys:
+    35 tiles, the last partial)."""
     cfg, tensors, types, gpu, ora = tiny
     long_ora = oracle.OracleModel(cfg, tensors, types, cap=1400)
     rng = np.random.default_rng(11)
@@ -78,7 +79,7 @@ def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
             gpu.profile(False)
         o = long_ora.forward(toks[prefix:], head_mode=1, vocab_ids=ids)
         assert np.array_equal(g, o), (prefix, n, H.rel_l2(g, o))
-        assert (n_fused, n_split) == ((cfg.n_layer, 0) if fused else (0, cfg.n_layer)), (prefix, n)
+        assert (n_fused, n_split) == ((cfg.n_layer, 0) if fused else (cfg.n_layer, cfg.n_layer)), (prefix, n)
 
 
 def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
