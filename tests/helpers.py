@@ -79,3 +79,32 @@ def shs_config_from_oracle(shs, cfg):
 
 CAPTURE_NAMES_PER_LAYER = ("attn_norm", "q_rope", "k_rope", "v", "attn_weighted", "attn_out", "post_attn",
                            "ffn_norm", "ffn_out", "output")
+
+
+# Unit block scales make the hot GEMM print its integer block sums: weights whose every
+# block quantizes with d = 1 (and m = 0) hold integer codes, activations whose every block
+# has max |x| = 127 quantize with d_a = 1 to codes equal to their values, so each scale
+# RN(d_w·d_a) is 1, the offset term is 0 and the fp32 chain acc = fma(I_b, 1, acc) adds exact
+# integers while |partial sums| < 2^24: y = Σ_b I_b exactly, I_b = Σ_k w_k·q_k.
+UNIT_RANGE = {2: (-8, 7), 3: (0, 15), 6: (-16, 15), 7: (0, 31), 8: (-127, 127)}
+
+
+def unit_scale_weights(oracle, qt, rows, cols, rng):
+    lo, hi = UNIT_RANGE[qt]
+    v = rng.integers(lo, hi + 1, (rows, cols)).astype(np.float32)
+    blk = v.reshape(rows, cols // 32, 32)
+    if qt in (2, 6):
+        blk[:, :, 0] = lo            # the max-|x| element fixes d = lo / lo = 1
+    elif qt in (3, 7):
+        blk[:, :, 0], blk[:, :, 1] = lo, hi  # min 0 and max 2^n − 1: d = 1, m = 0
+    else:
+        blk[:, :, 0] = hi            # max |x| = 127: d = 1
+    w = oracle.quantize(qt, v)
+    assert np.array_equal(oracle.dequantize(qt, w, rows * cols).reshape(rows, cols), v)
+    return w, v
+
+
+def unit_scale_activations(T, cols, rng):
+    x = rng.integers(-127, 128, (T, cols)).astype(np.float32)
+    x.reshape(T, cols // 32, 32)[:, :, 0] = 127
+    return x

@@ -234,3 +234,41 @@ def test_q5_blocks_with_every_fifth_bit_set_at_t512(lib, oracle, qt):
         y = m.forward(x)
         ref = oracle.matmul(qt, w, rows, cols, x, T)
         assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), T
+
+
+# With unit block scales (helpers.unit_scale_weights / unit_scale_activations) the GEMM's
+# outputs are exact sums of its int32 block sums.
+@pytest.mark.parametrize("qt", TYPES)
+def test_hot_gemm_single_block_outputs_are_the_int32_block_sums(lib, oracle, qt):
+    """K = 32: every output of the production GEMM (k_gemm, the same instantiations the model
+    runs) is one block's integer sum Σ w·q, against int64 brute force."""
+    rng = np.random.default_rng(70 + qt)
+    rows, cols, T = 256, 32, 96
+    w, v = H.unit_scale_weights(oracle, qt, rows, cols, rng)
+    x = H.unit_scale_activations(T, cols, rng)
+    y = lib.WeightMatrix(qt, rows, cols, w).forward(x)
+    ref = x.astype(np.int64) @ v.astype(np.int64).T
+    assert np.array_equal(y.astype(np.int64), ref) and np.all(y == ref)
+
+
+@pytest.mark.parametrize("qt,rows,cols,T", [
+    (2, 9216, 3072, 512),   # two token tiles per work-group, 2-block stages (the gate|up instantiation)
+    (2, 3072, 4096, 1024),  # one token tile, 4-block stages in a 3-slot ring (o and down)
+    (2, 256, 416, 64),      # 13 blocks: an odd last stage
+    (6, 256, 416, 512),
+    (7, 3072, 1024, 512),
+    (3, 1024, 2048, 128),
+    (8, 1024, 2048, 128),
+])
+def test_hot_gemm_unit_scale_outputs_are_exact_sums_of_block_sums(lib, oracle, qt, rows, cols, T):
+    """The whole K loop with unit scales: y = Σ_b I_b exactly, against float64 brute force
+    (exact: every product and partial sum is an integer far below 2^53). The precondition
+    Σ|w|·|q| < 2^24 keeps every partial sum of the fp32 chain exact."""
+    rng = np.random.default_rng(rows + cols + T + qt)
+    w, v = H.unit_scale_weights(oracle, qt, rows, cols, rng)
+    x = H.unit_scale_activations(T, cols, rng)
+    bound = np.abs(x).astype(np.float64) @ np.abs(v).astype(np.float64).T
+    assert bound.max() < 2 ** 24
+    y = lib.WeightMatrix(qt, rows, cols, w).forward(x)
+    ref = x.astype(np.float64) @ v.astype(np.float64).T
+    assert np.array_equal(y.astype(np.float64), ref)

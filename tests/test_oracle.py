@@ -506,3 +506,16 @@ def test_score_closed_form(oracle):
     s, y, n = oracle.score(logits, 3, 2)
     assert y == 3.0 and n == 0.5
     assert abs(s - 1 / (1 + math.exp(-(3.0 - 0.5)))) < 1e-6
+
+
+@pytest.mark.parametrize("qt", [2, 3, 6, 7, 8])
+def test_gemm_with_unit_block_scales_is_the_integer_product(oracle, qt):
+    """With every weight block at d = 1 (m = 0) and every activation block at d_a = 1, the
+    epilogue multiplies each int32 block sum by RN(1·1) = 1 and adds no offset, so the GEMM is
+    the integer product of the weights' and activations' values — a closed form that a wrong
+    nibble order, a dropped zero point or a misplaced fifth bit would break. 13 blocks."""
+    rng = np.random.default_rng(90 + qt)
+    w, v = H.unit_scale_weights(oracle, qt, 96, 416, rng)
+    x = H.unit_scale_activations(40, 416, rng)
+    y = oracle.matmul(qt, w, 96, 416, x, 40)
+    assert np.array_equal(y.astype(np.float64), x.astype(np.float64) @ v.astype(np.float64).T)
