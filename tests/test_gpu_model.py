@@ -368,6 +368,22 @@ def test_synthetic_model_round_trips_through_download(shs, oracle):
     again.close()
 
 
+def test_wide_hidden_rows_take_the_one_row_rmsnorm_blocks(shs, oracle):
+    """A hidden size of 5120: four rows' LDS (the row and its transposed squares) no longer fit
+    160 KB, so the RMSNorm launches run one row per block; the model stays bit-exact."""
+    cfg = oracle.make_config(n_layer=1, hidden=5120, n_head=40, n_kv_head=10, head_dim=128, ffn=1024, vocab=512)
+    scfg = H.shs_config_from_oracle(shs, cfg)
+    syn = shs.MinistralModel.synthetic(scfg, shs.Q4_0, shs.Q4_0, seed=8)
+    names = list(scfg.tensor_shapes(shs.Q4_0, shs.Q4_0))
+    tensors = {n: syn.download(n) for n in names}
+    types = {n: (0 if n.endswith("norm.weight") else 2) for n in names}
+    toks = np.random.default_rng(13).integers(0, cfg.vocab, 45)
+    got = syn.forward(toks)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=64)
+    assert np.array_equal(got, ora.forward(toks, head_mode=2))
+    syn.close()
+
+
 def test_device_exp_is_the_oracle_exp_bit_for_bit(shs, oracle):
     rng = np.random.default_rng(12)
     x = np.concatenate([np.linspace(-110, 90, 400001, dtype=np.float32),
