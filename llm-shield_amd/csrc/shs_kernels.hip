@@ -2796,8 +2796,9 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
     }
 
     // ---- softmax: thread (p, j, t) owns residue t of query row j in half p of the tiles.
-    // Both halves form e in place; then half 0 forms Σe in Kernels.Softmax's order over every
-    // tile; then both halves form w = e / Σe in place.
+    // Both halves form e in place, half 0 running the Σe chain of Kernels.Softmax's order
+    // over its own tiles as it goes; then half 0 continues the chain over half 1's tiles;
+    // then both halves form w = e / Σe in place.
     {
         const int p = tid >> 8, r = tid & 255;
         const int j = r >> 3, t = r & 7;
@@ -2812,9 +2813,25 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
         const int sw = att_swz(j, t);
         const int full_kt = ((it.pos0 + 1) & ~7) >> 5;
         const bool fast = !__any(qvalid && uniform);
-        const int kh = (n_kt + 1) >> 1;  // tiles [0, kh) in half 0, [kh, n_kt) in half 1
+        const int kh = n_kt >> 1;  // tiles [0, kh) in half 0, [kh, n_kt) in half 1
         const int k0 = p ? kh : 0, k1 = p ? n_kt : kh;
         constexpr int NB = 4;
+        // Σe: lane t sums its residue's keys below n8 in key order, the 8 lanes pairwise,
+        // then the keys n8 .. nq − 1 in order. Below full_kt every key is below n8.
+        float lane_sum = 0.0f, tail_e = 0.0f;
+        auto chain = [&](int kt, const float (&e)[4]) {
+            if (kt < full_kt) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) lane_sum = lane_sum + e[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int key = kt * 32 + t + 8 * k;
+                    lane_sum = key < n8 ? lane_sum + e[k] : lane_sum;
+                    tail_e = key >= n8 && key < nq ? e[k] : tail_e;
+                }
+            }
+        };
         for (int kt0 = k0; kt0 < k1; kt0 += NB) {
             float4 sv[NB];
 #pragma unroll
@@ -2837,14 +2854,12 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
                     }
                 }
                 *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
+                if (p == 0) chain(kt0 + qq, e);
             }
         }
         __syncthreads();  // every e is written
         if (p == 0) {
-            // Σe: lane t sums its residue's keys below n8 in key order, the 8 lanes pairwise,
-            // then the keys n8 .. nq − 1 in order
-            float lane_sum = 0.0f, tail_e = 0.0f;
-            for (int kt0 = 0; kt0 < n_kt; kt0 += NB) {
+            for (int kt0 = kh; kt0 < n_kt; kt0 += NB) {
                 float4 ev[NB];
 #pragma unroll
                 for (int qq = 0; qq < NB; qq++)
@@ -2853,12 +2868,7 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
                 for (int qq = 0; qq < NB; qq++) {
                     if (kt0 + qq >= n_kt) break;
                     const float e[4] = {ev[qq].x, ev[qq].y, ev[qq].z, ev[qq].w};
-#pragma unroll
-                    for (int k = 0; k < 4; k++) {
-                        const int key = (kt0 + qq) * 32 + t + 8 * k;
-                        lane_sum = key < n8 ? lane_sum + e[k] : lane_sum;
-                        tail_e = key >= n8 && key < nq ? e[k] : tail_e;
-                    }
+                    chain(kt0 + qq, e);
                 }
             }
             float total = vsum8_lanes(lane_sum);
