@@ -261,20 +261,23 @@ ISA_PATTERNS = [
     ("f16+fma", "2 fp16 x8 MFMAs + 32 independent FMAs", None),
     ("f32+fma", "1 fp32 1_2b MFMA + 32 independent FMAs", None),
     ("gemm_block", "one GEMM block on two token tiles: scale, 2 int8, 2 fp16, 32 dependent FMAs", None),
+    ("f32x2_chain", "4 v_mfma_f32_32x32x2_f32 on one accumulator (the attention's value chain)", 4),
+    ("f32x2+fma", "1 v_mfma_f32_32x32x2_f32 + 16 independent FMAs", None),
 ]
 
 
 def isa_probe(iters=20000):
     """SIMD cycles per iteration of each probe pattern (shader clock, from the span of each
-    work-group's waves), for one wave per SIMD on one CU and for three waves per SIMD on every
-    CU (the GEMM's occupancy)."""
+    work-group's waves), for one wave per SIMD on one CU, and for two (the attention's
+    occupancy) and three waves per SIMD (the GEMM's) on every CU."""
     import ctypes as C
     lib = C.CDLL(str(ROOT / "llm-shield_amd" / "libshs_probe.so"))
     assert lib.shs_probe_count() == len(ISA_PATTERNS)
     rows = []
     for p, (name, what, per) in enumerate(ISA_PATTERNS):
         row = {"pattern": name, "issues": what}
-        for label, blocks, waves in (("1_wave_per_simd", 1, 4), ("3_waves_per_simd_all_cus", 256, 12)):
+        for label, blocks, waves in (("1_wave_per_simd", 1, 4), ("2_waves_per_simd_all_cus", 256, 8),
+                                     ("3_waves_per_simd_all_cus", 256, 12)):
             cyc, mhz = C.c_double(), C.c_double()
             rc = lib.shs_probe_run(p, blocks, waves, iters, C.byref(cyc), C.byref(mhz))
             if rc != 0:

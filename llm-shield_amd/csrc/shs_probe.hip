@@ -1,5 +1,5 @@
-// Instruction-issue probes for the GEMM's design choices on gfx950: how many cycles each MFMA
-// form and the fp32 VALU FMA take per wave, and which of them overlap when one wave issues
+// Instruction-issue probes for the GEMM's and the attention's design choices on gfx950: how
+// many cycles each MFMA form and the fp32 VALU FMA take per wave, and which of them overlap when one wave issues
 // them together. Built as its own library (libshs_probe.so) beside the product; bench.py
 // --isa-probe runs every pattern and prints the table. Nothing here touches memory except
 // the one result record per wave (and a sink store that never executes).
@@ -27,6 +27,8 @@ enum {
     P_F32_FMA,        // 1 fp32 1_2b MFMA + 32 independent FMAs
     P_GEMM_BLOCK,     // one block of the GEMM's K loop on two token tiles: scale MFMA, 2 int8,
                       // 2 fp16 conversions, 32 FMAs that read their results
+    P_F32X2_CHAIN,    // 4 v_mfma_f32_32x32x2_f32 on one accumulator (the attention's value chain)
+    P_F32X2_FMA,      // 1 v_mfma_f32_32x32x2_f32 + 16 independent FMAs (the score phase's mix)
     P_COUNT
 };
 
@@ -124,6 +126,13 @@ __global__ __launch_bounds__(768) void k_probe(int iters, uint64_t* out, float* 
             }
             keep(cf[0]);
             keep(cf[1]);
+        } else if constexpr (P == P_F32X2_CHAIN) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) cf[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa, fb, cf[0], 0, 0, 0);
+        } else if constexpr (P == P_F32X2_FMA) {
+            cf[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa, fb, cf[0], 0, 0, 0);
+#pragma unroll
+            for (int k = 0; k < 16; k++) x[k] = fmaf(x[k], fa, fb);
         }
     }
     const uint64_t t1 = __builtin_amdgcn_s_memtime();
@@ -167,6 +176,8 @@ hipError_t launch_pattern(int p, int blocks, int waves, int iters, uint64_t* out
     case P_F16_FMA: return launch<P_F16_FMA>(blocks, waves, iters, out, sink);
     case P_F32_FMA: return launch<P_F32_FMA>(blocks, waves, iters, out, sink);
     case P_GEMM_BLOCK: return launch<P_GEMM_BLOCK>(blocks, waves, iters, out, sink);
+    case P_F32X2_CHAIN: return launch<P_F32X2_CHAIN>(blocks, waves, iters, out, sink);
+    case P_F32X2_FMA: return launch<P_F32X2_FMA>(blocks, waves, iters, out, sink);
     default: return hipErrorInvalidValue;
     }
 }
