@@ -2645,14 +2645,22 @@ __device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc,
     if (!vwave) return;
     wread(0, wa);
     // iteration kt: `cur` holds V(kt) (V(kt + 1) in flight), `w` tile kt's weights; it reads
-    // tile kt + 1's weights, issues tile kt's 16 MFMAs, then loads V(kt + 2) into `cur`
+    // tile kt + 1's weights, then issues tile kt's 16 MFMAs, loading V(kt + 2) into `cur`
     auto step = [&](int kt, VOps& cur, WOps& w, WOps& wn) {
         wread(kt + 1, wn);
+        const int rows = n_keys - (kt + 2) * 32;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(vbase + (int64_t)(kt + 2) * 32 * ATT_HD), 0, rows > 0 ? rows * (ATT_HD * 4) : 0,
+            0x00020000);
         __builtin_amdgcn_sched_barrier(0);
+        // V(kt + 2) into `cur`, each load issued in the shadow of the MFMA that last reads its
+        // register (16 loads issued back to back would hold up the next tile's first MFMA)
 #pragma unroll
-        for (int c = 0; c < 16; c++) o = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[c], w.w[c], o, 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        vload(kt + 2, cur);
+        for (int c = 0; c < 16; c++) {
+            o = __builtin_amdgcn_mfma_f32_32x32x2f32(cur.a[c], w.w[c], o, 0, 0, 0);
+            cur.a[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff + c * (2 * ATT_HD * 4), 0, 0));
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
     int kt = 0;
     for (; kt + 1 < n_kt; kt += 2) {
