@@ -115,6 +115,48 @@ def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
         gpu.close()
 
 
+def test_non_finite_score_rows_take_the_uniform_softmax(shs, oracle):
+    """Kernels.Softmax weighs every key of a row equally when the row's maximum is not
+    finite (Kernels.cs:157-200). A huge attention-norm gain in layer 0 makes q·k overflow:
+    at 1e19 some rows overflow and others stay finite, at 1e20 almost all overflow. The
+    fused kernel (70 tokens), the three-kernel path (1300 tokens) and the decode-width
+    kernels (one more token) must all match the oracle bit for bit."""
+    cfg = oracle.make_config(**TINY)
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=7)
+    rng = np.random.default_rng(23)
+    ids = [3, 100, 400]
+    flt_max = float(np.finfo(np.float32).max)
+    for gain, mixed in ((1e19, True), (1e20, False)):
+        t2 = dict(tensors)
+        t2["blk.0.attn_norm.weight"] = (tensors["blk.0.attn_norm.weight"] * np.float32(gain)).astype(np.float32)
+        gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), t2, types)
+        ora = oracle.OracleModel(cfg, t2, types, cap=1400)
+        try:
+            for n in (70, 1300):
+                toks = rng.integers(0, cfg.vocab, n)
+                gpu.reset_kv_cache()
+                ora.reset()
+                g = gpu.forward_selected(toks, ids)
+                cap = {}
+                o = ora.forward(toks, head_mode=1, vocab_ids=ids, capture=lambda nm, a: cap.__setitem__(nm, a))
+                assert np.array_equal(g, o, equal_nan=True), (gain, n, H.rel_l2(g, o))
+                # the premise: layer 0's unscaled scores (exact in float64) pass FLT_MAX in some rows
+                q = cap["blk.0.q_rope"][:, :cfg.head_dim].astype(np.float64)
+                k = cap["blk.0.k_rope"][:, :cfg.head_dim].astype(np.float64)
+                s = np.abs(q @ k.T)
+                row_max = np.array([s[i, :i + 1].max() for i in range(n)])
+                over = row_max > flt_max
+                assert over.any(), (gain, n)
+                if mixed:
+                    assert not over.all(), (gain, n)
+            step = rng.integers(0, cfg.vocab, 1)
+            g = gpu.forward(step)
+            o = ora.forward(step, head_mode=2)
+            assert np.array_equal(g, o, equal_nan=True), (gain, H.rel_l2(g, o))
+        finally:
+            gpu.close()
+
+
 def test_packed_batch_of_decode_width_prompts_matches_the_oracle(shs, oracle, tiny):
     """A packed batch of 1-4-token prompts: every item is decode width, so attention runs
     k_attn_dec_scores + k_attn_dec_pv over 5 items, while the GEMMs (T = 12 > 4) take k_gemm:
