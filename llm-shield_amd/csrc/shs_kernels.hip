@@ -1272,12 +1272,21 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
         quant_block_pair(yv, h, ao, (tt0 + u) * 32 + j, fti);
         return;
     }
+    // q|k|v stages its output tiles through the ring, which is free once every wave (active
+    // or not) has left the K loop
+    if constexpr (MODE == GEMM_QKV) __syncthreads();
     if (!active) return;
     if constexpr (MODE == GEMM_QKV) {
         // Rope.Apply on adjacent pairs (x0, x1) → (x0c − x1s, x0s + x1c), unfused, then the
         // query position scale (MinistralModel.cs:442-482); StoreKeys/StoreValues put k and v
         // at the token's cache slot. A tile lies inside one head (hd is a multiple of 32).
+        // The tile goes through this wave's part of the ring as [token][32 features], so that
+        // every store below writes whole 128-byte rows (8 tokens per instruction).
+        constexpr int XLD = 36;  // floats per staged token row: rows start 4 banks apart
+        static_assert(NS * L::BYTES >= 4 * TT * 32 * XLD * 4, "the ring holds the staged tiles");
+        float* X = reinterpret_cast<float*>(ring) + wave * TT * 32 * XLD;
         const int hrow = rt * 32 / ra.hd, e0 = rt * 32 % ra.hd;
+        const bool rot = hrow < ra.n_head + ra.n_kv, query = hrow < ra.n_head;
 #pragma unroll
         for (int u = 0; u < TT; u++) {
             const int token = (tt0 + u) * 32 + j;
@@ -1287,7 +1296,7 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
             for (int g = 0; g < 4; g++) {
                 const int e = e0 + 8 * g + 4 * h;  // element of the head held in acc[u][4g..4g+3]
                 float v[4] = {acc[u][4 * g], acc[u][4 * g + 1], acc[u][4 * g + 2], acc[u][4 * g + 3]};
-                if (hrow < ra.n_head + ra.n_kv) {
+                if (rot) {
 #pragma unroll
                     for (int k = 0; k < 2; k++) {
                         const int pi = e / 2 + k;
@@ -1301,20 +1310,35 @@ __global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs
                         }
                     }
                 }
-                float* dst;
-                if (hrow < ra.n_head) {
+                if (query) {
                     const float qs = ra.qscale[p];
                     if (qs != 1.0f) {
 #pragma unroll
                         for (int k = 0; k < 4; k++) v[k] = v[k] * qs;
                     }
-                    dst = y + (int64_t)token * ldy + rt * 32 + 8 * g + 4 * h;
-                } else if (hrow < ra.n_head + ra.n_kv) {
-                    dst = ra.kc + ((int64_t)(hrow - ra.n_head) * ra.cap + ra.slot0 + token) * ra.hd + e;
-                } else {
-                    dst = ra.vc + ((int64_t)(hrow - ra.n_head - ra.n_kv) * ra.cap + ra.slot0 + token) * ra.hd + e;
                 }
-                *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(X + (u * 32 + j) * XLD + 8 * g + 4 * h) = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        }
+        // this wave's rows are in the LDS (only this wave reads them)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int c4 = 4 * (lane & 7);
+#pragma unroll
+        for (int u = 0; u < TT; u++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = (lane >> 3) + 8 * i;
+                const int token = (tt0 + u) * 32 + r;
+                if (u >= nv || token >= a.T) continue;
+                const float4 v = *reinterpret_cast<const float4*>(X + (u * 32 + r) * XLD + c4);
+                float* dst;
+                if (query)
+                    dst = y + (int64_t)token * ldy + rt * 32 + c4;
+                else if (rot)
+                    dst = ra.kc + ((int64_t)(hrow - ra.n_head) * ra.cap + ra.slot0 + token) * ra.hd + e0 + c4;
+                else
+                    dst = ra.vc + ((int64_t)(hrow - ra.n_head - ra.n_kv) * ra.cap + ra.slot0 + token) * ra.hd + e0 + c4;
+                *reinterpret_cast<float4*>(dst) = v;
             }
         }
         return;
