@@ -896,8 +896,17 @@ __device__ __forceinline__ void quant_block_pair(const float* y, int h, const Ac
     }
 }
 
+// Work-groups per CU the LDS ring admits (at most 3, the register budget's target): Q8_0's
+// two-tile ring (≈61 KB) admits 2.
+template <int TYPE, int TT, int BPS>
+constexpr int gemm_wg_per_cu()
+{
+    typedef GemmSlot<TYPE, TT, BPS> L;
+    return 3 * L::NS * L::BYTES <= 160 * 1024 ? 3 : 2;
+}
+
 template <int TYPE, int TT, int MODE, int BPS>
-__global__ __launch_bounds__(256, 3) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
+__global__ __launch_bounds__(256, (gemm_wg_per_cu<TYPE, TT, BPS>())) void k_gemm(const uint8_t* __restrict__ wqs, const uint32_t* __restrict__ wqh,
                                                  const float* __restrict__ wd, const float* __restrict__ wm,
                                                  int ntiles, int B, ActQ8 a, float* __restrict__ y, int ldy, int N,
                                                  int n_tg, ActQ8 ao, int n_ft, RopeArgs ra)
