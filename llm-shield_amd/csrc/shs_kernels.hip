@@ -6,12 +6,38 @@
 // 376-418), RMSNorm's accumulation order (Kernels.cs:26-61) and RoPE's rotation
 // (Rope.cs:112-135). The file is compiled with -ffp-contract=off; every fma is explicit.
 #include "shs_kernels.h"
+#include <atomic>
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
 #include <math.h>
 
 namespace shs {
+
+// A kernel's dynamic LDS beyond 64 KB must be allowed with hipFuncSetAttribute, which HIP keeps
+// per device. One LdsLimit per kernel remembers the largest size allowed on each device, so the
+// call is made once per size increase; handles on several host threads may launch at once (a
+// lock-free check, then the raise under a mutex, always to the largest size asked so far).
+struct LdsLimit {
+    static constexpr int MAX_DEVICES = 16;
+    std::atomic<size_t> allowed[MAX_DEVICES] = {};
+    std::mutex mu;
+    hipError_t raise(const void* fn, size_t bytes)
+    {
+        if (bytes <= (64u << 10)) return hipSuccess;
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        std::atomic<size_t>* a = dev >= 0 && dev < MAX_DEVICES ? &allowed[dev] : nullptr;
+        if (a && a->load(std::memory_order_acquire) >= bytes) return hipSuccess;
+        std::lock_guard<std::mutex> lock(mu);
+        const size_t target = a ? std::max(bytes, a->load(std::memory_order_relaxed)) : bytes;
+        e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)target);
+        if (e == hipSuccess && a) a->store(target, std::memory_order_release);
+        return e;
+    }
+};
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -619,13 +645,9 @@ static hipError_t rmsnorm_launch(const float* x, int ldx, const float* w, float 
                                  float* y_opt, hipStream_t s, size_t lds_row)
 {
     const size_t lds = ROWS * lds_row;
-    static size_t attr = 0;
-    if (lds > attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_rmsnorm_quant<ROWS>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr = lds;
-    }
+    static LdsLimit limit;
+    hipError_t e = limit.raise(reinterpret_cast<const void*>(k_rmsnorm_quant<ROWS>), lds);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_rmsnorm_quant<ROWS>, dim3(a.Tpad / ROWS), dim3(256 * ROWS), lds, s, x, ldx, w, eps, n, a,
                        y_opt);
     return hipGetLastError();
@@ -2000,11 +2022,9 @@ static hipError_t narrow_launch(const DevMatrix& w, const ActQ8& a, float* y, in
     constexpr bool OFF = TYPE == SHS_TYPE_Q4_1 || TYPE == SHS_TYPE_Q5_1;
     const int n_wg = MODE == GEMM_SWIGLU ? n_ft : w.tiles * (32 / R);
     const size_t shm = narrow_lds_bytes(R, w.blocks, NT, OFF) + (nin.x ? narrow_norm_lds_bytes(w.blocks) : 0);
-    if (shm > (64u << 10)) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemm_narrow<TYPE, NT, MODE, R>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
-        if (e != hipSuccess) return e;
-    }
+    static LdsLimit limit;
+    hipError_t e = limit.raise(reinterpret_cast<const void*>(k_gemm_narrow<TYPE, NT, MODE, R>), shm);
+    if (e != hipSuccess) return e;
     dim3 grid((unsigned)((n_wg + 7) / 8 * 8)), block(256);
     hipLaunchKernelGGL((k_gemm_narrow<TYPE, NT, MODE, R>), grid, block, shm, s, w.qs, w.qh, w.d, w.m, w.rows,
                        w.blocks, n_wg, a, y, ldy, ao, n_ft, ra, nin);
@@ -3062,13 +3082,9 @@ hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const flo
     if (codes && (codes->B != n_head * ATT_HD / 32 || !codes->q)) return hipErrorInvalidValue;
     const ActQ8 ao = codes ? *codes : ActQ8();
     const size_t lds = ((size_t)kt_cap * 1024 + ATT_RMAX + 32 + ATT_QLDS) * sizeof(float);
-    static int attr_set = 0;
-    if (attr_set < (int)lds) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_fused),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr_set = (int)lds;
-    }
+    static LdsLimit limit;
+    hipError_t e = limit.raise(reinterpret_cast<const void*>(k_attn_fused), lds);
+    if (e != hipSuccess) return e;
     const int n_groups = n_items * n_kv;
     const unsigned grid = (unsigned)(((n_groups + 7) / 8) * 32);
     hipLaunchKernelGGL(k_attn_fused, dim3(grid), dim3(ATT_THREADS), lds, s, q, ldq, kc, vc, cap, items, n_items, n_head, n_kv,
@@ -3402,22 +3418,17 @@ hipError_t launch_attn_decode(const float* q, int ldq, const float* kc, const fl
     const int G = n_head / n_kv;
     const int n_chunks = (max_keys + DEC_KT - 1) / DEC_KT;
     const size_t shs = dec_scores_lds(G, max_qc);
-    if (shs > (64u << 10)) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_dec_scores),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)shs);
-        if (e != hipSuccess) return e;
-    }
+    static LdsLimit scores_limit, pv_limit;
+    hipError_t e = scores_limit.raise(reinterpret_cast<const void*>(k_attn_dec_scores), shs);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_dec_scores, dim3((unsigned)(n_items * n_kv * n_chunks)), dim3(256), shs, s, q, ldq, kc,
                        cap, items, n_head, n_kv, n_chunks, scale, scratch);
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int ld_s = (max_keys + 15) & ~15;  // the value loop reads weights 16 at a time
     const size_t shp = dec_pv_lds(max_qc, ld_s);
-    if (shp > (64u << 10)) {
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_attn_dec_pv), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)shp);
-        if (e != hipSuccess) return e;
-    }
+    e = pv_limit.raise(reinterpret_cast<const void*>(k_attn_dec_pv), shp);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_attn_dec_pv, dim3((unsigned)(n_items * n_head * (ATT_HD / 32))), dim3(256), shp, s, vc, cap,
                        items, n_head, n_kv, ld_s, max_qc, scratch, ctx, ldc, codes ? *codes : ActQ8());
     return hipGetLastError();

@@ -157,6 +157,55 @@ def test_non_finite_score_rows_take_the_uniform_softmax(shs, oracle):
             gpu.close()
 
 
+def test_two_handles_on_two_host_threads_match_their_serial_results(shs, oracle):
+    """Separate handles may run concurrently, each on its own stream (ShieldstralModerator.cs:46,
+    MinistralModel.cs:21-22): two handles of a model, driven from two host threads at once
+    through prefill and decode, give the same bits as each run alone. The first passes raise
+    the kernels' LDS limits, which the two threads share."""
+    import threading
+
+    cfg = oracle.make_config(n_layer=2, hidden=256, n_head=4, n_kv_head=1, head_dim=128, ffn=512, vocab=512)
+    tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=29)
+    rng = np.random.default_rng(31)
+    prompts = [rng.integers(0, cfg.vocab, n) for n in (600, 1200)]
+    steps = [rng.integers(0, cfg.vocab, 3) for _ in prompts]
+    handles = [shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types) for _ in prompts]
+
+    def run(m, prompt, step):
+        m.reset_kv_cache()
+        out = [m.forward(prompt)]
+        for t in step:
+            out.append(m.forward([t]))
+        return out
+
+    try:
+        serial = [run(m, p, st) for m, p, st in zip(handles, prompts, steps)]
+        results = [None, None]
+        errors = []
+        barrier = threading.Barrier(2)
+
+        def worker(i):
+            try:
+                barrier.wait()
+                for _ in range(3):
+                    results[i] = run(handles[i], prompts[i], steps[i])
+            except Exception as e:  # reported below
+                errors.append(e)
+
+        threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+        for th in threads:
+            th.start()
+        for th in threads:
+            th.join()
+        assert not errors, errors
+        for i in range(2):
+            for a, b in zip(results[i], serial[i]):
+                assert np.array_equal(a, b), i
+    finally:
+        for m in handles:
+            m.close()
+
+
 def test_packed_batch_of_decode_width_prompts_matches_the_oracle(shs, oracle, tiny):
     """A packed batch of 1-4-token prompts: every item is decode width, so attention runs
     k_attn_dec_scores + k_attn_dec_pv over 5 items, while the GEMMs (T = 12 > 4) take k_gemm:
