@@ -1433,17 +1433,19 @@ static hipError_t gemm_launch(const DevMatrix& w, const ActQ8& a, float* y, int 
 template <int TYPE, int TT, int MODE, int BPS>
 static int gemm_slots()
 {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64] = {};  // threads that race store the same value
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cached[dev] == 0) {
+    int slots = cached[dev].load(std::memory_order_relaxed);
+    if (slots == 0) {
         int per_cu = 0, n_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemm<TYPE, TT, MODE, BPS>, 256, 0) != hipSuccess ||
             hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
             return 0;
-        cached[dev] = per_cu * n_cu;
+        slots = per_cu * n_cu;
+        cached[dev].store(slots, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return slots;
 }
 
 // Token tiles per work-group: 2 when its work-groups fill their last round of resident
@@ -3027,9 +3029,13 @@ static dim3 attn_blocks(int n_work, int per_cu, int n_cu)
 
 int attn_score_slots(int n_cu)
 {
-    static int per_cu = 0;  // the same on every gfx950 device
-    if (per_cu == 0 && hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_attn_scores, 256, 0) != hipSuccess)
-        per_cu = 2;
+    static std::atomic<int> cached{0};  // the same on every gfx950 device; racing threads store the same value
+    int per_cu = cached.load(std::memory_order_relaxed);
+    if (per_cu == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_attn_scores, 256, 0) != hipSuccess || per_cu <= 0)
+            per_cu = 2;
+        cached.store(per_cu, std::memory_order_relaxed);
+    }
     return per_cu * n_cu;
 }
 
