@@ -2617,25 +2617,30 @@ __device__ __forceinline__ void attn_pv_work(int idx, int dt, int kvh, const flo
                 make_float4(o[sl][4 * g], o[sl][4 * g + 1], o[sl][4 * g + 2], o[sl][4 * g + 3]);
 }
 
-// Scores, softmax and values of one (item, query head) in one block, the item's scores kept
-// in the LDS between the phases (MinistralModel.AttendGroup, MinistralModel.cs:372-440, in
-// the floating-point order stated above):
-//  * scores: wave w computes whole 32×32 tiles w, w + 4, … — the eight Dot4 chains on
-//    v_mfma_f32_32x32x2f32 as in attn_scores_work, its q row in registers and its K
-//    operands loaded from global memory three chain steps ahead into a register ring. A K
-//    row is read once per block, and the phase has no barrier. vsum8, the scale and the
-//    row maxima (NaN-propagating, so a NaN score reaches the softmax as a NaN maximum)
-//    follow in registers; the tile goes into the LDS in the softmax layout;
-//  * softmax: thread (j, t) owns residue t of query row j, as in attn_softmax_work —
-//    Σe in Kernels.Softmax's order, then w = e / Σe over the row's LDS copy;
-//  * values: wave w runs the ordered FMA chain of 32-dimension slice w over all keys, its V
-//    elements loaded from global memory two tiles ahead, its weights from the LDS one
-//    tile ahead; no barrier either.
+// Scores, softmax and values of one (item, query head) in one block of eight waves, the
+// item's scores kept in the LDS between the phases (MinistralModel.AttendGroup,
+// MinistralModel.cs:372-440, in the floating-point order stated above):
+//  * scores: the block's 32 query rows go to the LDS once, as the operands each chain step
+//    reads; wave w computes whole 32×32 tiles w, w + 8, … — the eight Dot4 chains on
+//    v_mfma_f32_32x32x2f32 as in attn_scores_work, its K operands loaded from global memory
+//    three chain steps ahead into a register ring (a K row is read once per block, and the
+//    phase has no barrier). vsum8, the scale and the row maxima (NaN-propagating, so a NaN
+//    score reaches the softmax as a NaN maximum) follow in registers; the tile goes into
+//    the LDS in the softmax layout;
+//  * softmax: thread (p, j, t) owns residue t of query row j in half p of the tiles, as in
+//    attn_softmax_work: both halves form e in place, half 0 runs the Σe chain in
+//    Kernels.Softmax's order over its tiles as it goes and then over half 1's, and both
+//    halves form w = e / Σe in place;
+//  * values: wave w < 4 runs the ordered FMA chain of 32-dimension slice w over all keys,
+//    its V elements loaded from global memory two tiles ahead (each load issued in the
+//    shadow of the MFMA that last reads its register), its weights from the LDS one tile
+//    ahead; no barrier either.
 // LDS: kt_cap score tiles of 1024 floats, [query j][slot][k] with residue t in slot
-// t ^ (j & 7) (conflict-free float4 writes, 2-way float4 reads), then the four waves'
-// 32 row maxima. Blocks map to (KV-head group, head in group) so that the group's heads —
-// which read the same K and V rows — share an XCD and start together: block b runs group
-// 8·(b >> 5) + (b & 7) (groups longest first) and head (b >> 3) & 3 of it.
+// t ^ (j & 7) (conflict-free float4 writes, 2-way float4 reads), then the eight waves'
+// 32 row maxima, the 32 row sums and the query operands. Blocks map to (KV-head group, head
+// in group) so that the group's heads — which read the same K and V rows — share an XCD and
+// start together: block b runs group 8·(b >> 5) + (b & 7) (groups longest first) and head
+// (b >> 3) & 3 of it.
 constexpr int ATT_THREADS = 512;  // eight waves: two per SIMD in the score and softmax phases
 constexpr int ATT_RMAX = (ATT_THREADS / 64) * 32;  // floats of the row maxima after the score tiles
 constexpr int ATT_QLDS = 32 * ATT_HD;              // floats of the query rows after the maxima and Σe
