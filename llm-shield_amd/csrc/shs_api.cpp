@@ -366,10 +366,10 @@ struct shs_model {
     Buf chunks, counters;  // counters: the attention kernels' three work counters
     int n_chunks = 0;
     int n_cu = 0;          // compute units of the device (persistent kernel sizing)
-    int fused_kt = 0;      // most key tiles an item may have for the fused softmax + values kernel
+    int fused_kt = 0;      // score tiles a fused-kernel block can hold in its LDS (a longer item spills the rest)
     int max_kt = 0;        // key tiles of the longest placed item
     int max_kt_fused = 0;  // key tiles of the longest item the fused kernel takes
-    int n_long = 0;        // placed items past fused_kt key tiles: the first n_long of the list
+    int n_long = 0;        // placed items past ATT_FUSED_MAX_KT key tiles: the first n_long of the list
     int max_lds = 0;       // LDS bytes a block may use (opt-in)
     int max_qc = 0;        // queries of the widest placed item
     int max_keys = 0;      // keys of the longest placed item
@@ -1104,10 +1104,11 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
                                            c.head_dim, scale, m->max_qc, m->max_keys, scr, ctx, qdim,
                                            cap_on ? nullptr : &ac, m->stream));
             } else {
-                // Items past the fused kernel's key tiles (the first n_long of the list) take the
+                // Items past ATT_FUSED_MAX_KT key tiles (the first n_long of the list) take the
                 // three kernels through the score scratch; the rest the fused kernel, whose block
-                // holds an item's scores in its LDS and which, without capture, writes the o
-                // projection's activation codes itself. The two sets of items write disjoint rows.
+                // holds an item's first score tiles in its LDS and the rest in the item's scratch
+                // region, and which, without capture, writes the o projection's activation codes
+                // itself. The two sets of items write disjoint rows and regions.
                 const int n_long = m->n_long, n_fused = n_items - n_long;
                 if (n_long > 0) {
                     {
@@ -1129,9 +1130,11 @@ shs_status run_layers(shs_model* m, int T, float* kc_all, float* vc_all, int cap
                 }
                 if (n_fused > 0) {
                     Timed tk(m->prof, "k_attn_fused", 2 * (attn_ops - long_ops), m->stream, "attention");
+                    // the LDS holds up to fused_kt tiles; past them the spilling instantiation runs
+                    const int kt_cap = std::min(m->max_kt_fused, m->fused_kt);
                     HIP_TRY(launch_attn_fused(qkv, ldqkv, kc, vc, cap, items_dev + n_long, n_fused, c.n_head,
-                                              c.n_kv_head, c.head_dim, scale, ctx, qdim, cap_on ? nullptr : &ac,
-                                              m->max_kt_fused, m->stream));
+                                              c.n_kv_head, c.head_dim, scale, ctx, qdim, cap_on ? nullptr : &ac, kt_cap,
+                                              m->max_kt_fused > kt_cap ? scr : nullptr, m->stream));
                 }
             }
         }
@@ -1283,10 +1286,12 @@ shs_status place_items(shs_model* m, std::vector<AttnItem>& items)
     auto tiles = [](const AttnItem& it) { return (it.pos0 + it.q_count + 31) / 32; };
     std::stable_sort(items.begin(), items.end(),
                      [&](const AttnItem& a, const AttnItem& b) { return tiles(a) < tiles(b); });
-    const int fused_kt = m->fused_kt;
-    std::stable_partition(items.begin(), items.end(), [&](const AttnItem& it) { return tiles(it) > fused_kt; });
+    // items past ATT_FUSED_MAX_KT key tiles take the three-kernel path; the fused kernel holds
+    // up to fused_kt tiles of the rest in its LDS and their later tiles in their regions
+    const int fused_max = m->fused_kt > 0 ? ATT_FUSED_MAX_KT : 0;
+    std::stable_partition(items.begin(), items.end(), [&](const AttnItem& it) { return tiles(it) > fused_max; });
     int n_long = 0;
-    while (n_long < (int)items.size() && tiles(items[n_long]) > fused_kt) n_long++;
+    while (n_long < (int)items.size() && tiles(items[n_long]) > fused_max) n_long++;
     int kChunk = 4;
     {
         const int64_t slots = std::max(1, attn_score_slots(m->n_cu));

@@ -170,12 +170,16 @@ hipError_t launch_attn_softmax(const AttnItem* items, int n_items, int n_head, i
 hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n_items, int n_head, int n_kv,
                           const float* scratch, float* ctx, int ldc, const ActQ8* codes, int* counters, int n_cu,
                           hipStream_t s);
-// Scores, softmax and values in one kernel (in place of the three above) for passes whose
-// every item has at most kt_cap key tiles: one block per (item, query head) holds the item's
-// scores in kt_cap LDS tiles; kt_cap at most attn_fused_kt_limit(the device's LDS per block).
+// Scores, softmax and values in one kernel (in place of the three above): one block per
+// (item, query head) holds the item's first kt_cap score tiles in its LDS; kt_cap at most
+// attn_fused_kt_limit(the device's LDS per block). When an item has more key tiles, `spill`
+// (the scratch regions place_items lays out) holds its later tiles; with spill null every
+// item must fit kt_cap tiles. Items of up to ATT_FUSED_MAX_KT key tiles take it; longer ones
+// the three kernels above.
+constexpr int ATT_FUSED_MAX_KT = 96;
 hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
                              int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
-                             const ActQ8* codes, int kt_cap, hipStream_t s);
+                             const ActQ8* codes, int kt_cap, float* spill, hipStream_t s);
 int attn_fused_kt_limit(int max_lds_bytes);
 // Attention for items of at most ATT_DEC_MAX_Q queries (decode), at most 4 query heads per
 // KV head: a score kernel over (item, KV head, 64-key chunk) writing the scores to the

@@ -2651,8 +2651,10 @@ __device__ __forceinline__ int att_swz(int j, int t) { return j * 32 + ((t ^ (j 
 // block's LDS score tiles S. Lane (j, h) feeds V[key 2c + h][32·wave + j] as the A operand
 // and w[j][2c + h] as the B operand of step c of a tile, so each v_mfma_f32_32x32x2f32 is
 // two consecutive keys of every chain ctx[j][d] = fma(v, w, ctx[j][d]).
+template <bool SPILL>
 __device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc, int cap, const AttnItem& it, int kvh,
                                                    int head, int n_kt, int n_keys, const float* S,
+                                                   const float* __restrict__ G, int kt_lds,
                                                    float* __restrict__ ctx, int ldc, const ActQ8& ao)
 {
     const int tid = threadIdx.x;
@@ -2681,15 +2683,23 @@ __device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc,
     };
     auto wread = [&](int kt, WOps& op) {
         // residue 2m + h (m = c & 3), k = c >> 2 of the tile's rows; past the last tile the
-        // last is read again, unused
-        const float* st = S + min(kt, n_kt - 1) * 1024;
+        // last is read again, unused. Tiles from kt_lds on live in the block's spill region.
+        const int k = min(kt, n_kt - 1);
+        float4 v[4];
+        if (!SPILL || k < kt_lds) {
+#pragma unroll
+            for (int m = 0; m < 4; m++) v[m] = *reinterpret_cast<const float4*>(S + k * 1024 + att_swz(j, 2 * m + h));
+        } else {
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                v[m] = *reinterpret_cast<const float4*>(G + (int64_t)k * 1024 + att_swz(j, 2 * m + h));
+        }
 #pragma unroll
         for (int m = 0; m < 4; m++) {
-            const float4 v = *reinterpret_cast<const float4*>(st + att_swz(j, 2 * m + h));
-            op.w[m] = v.x;
-            op.w[m + 4] = v.y;
-            op.w[m + 8] = v.z;
-            op.w[m + 12] = v.w;
+            op.w[m] = v[m].x;
+            op.w[m + 4] = v[m].y;
+            op.w[m + 8] = v[m].z;
+            op.w[m + 12] = v[m].w;
         }
     };
     v16f o;
@@ -2747,12 +2757,16 @@ __device__ __forceinline__ void attn_values_stream(const float* __restrict__ vc,
         *reinterpret_cast<float4*>(outp + 8 * gq + 4 * h) = make_float4(o[4 * gq], o[4 * gq + 1], o[4 * gq + 2], o[4 * gq + 3]);
 }
 
+// SPILL = false: every item fits the LDS tiles (kt_cap ≥ its key tiles), and the kernel has no
+// spill path at all; SPILL = true: items past kt_cap keep their later tiles in `spill`.
+template <bool SPILL>
 __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __restrict__ q, int ldq,
                                                               const float* __restrict__ kc,
                                                               const float* __restrict__ vc, int cap,
                                                               const AttnItem* __restrict__ items, int n_items,
                                                               int n_head, int n_kv, float scale,
-                                                              float* __restrict__ ctx, int ldc, ActQ8 ao, int kt_cap)
+                                                              float* __restrict__ ctx, int ldc, ActQ8 ao, int kt_cap,
+                                                              float* __restrict__ spill)
 {
     extern __shared__ float4 att_lds4[];
     float* S = reinterpret_cast<float*>(att_lds4);
@@ -2769,6 +2783,10 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
     const AttnItem it = items[idx];
     const int n_kt = att_tiles(it);
     const int n_keys = it.pos0 + it.q_count;
+    // Tiles 0 .. kt_cap − 1 live in the LDS; an item with more keeps tiles kt_cap .. n_kt − 1 in
+    // its scratch region for this head (the region the three-kernel path uses), read back by
+    // this block only, after the barriers that order its phases.
+    float* G = SPILL ? spill + it.s_off + (int64_t)(kvh * 4 + hg) * n_kt * 1024 : nullptr;
 
     // ---- scores
     {
@@ -2840,11 +2858,19 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
                 sc[r] = (a + bsum) * scale;
             }
             // residue 2m + h of query j is (sc[m], sc[m+4], sc[m+8], sc[m+12])
-            float* out = S + kt * 1024;
+            if (!SPILL || kt < kt_cap) {
+                float* out = S + kt * 1024;
 #pragma unroll
-            for (int m = 0; m < 4; m++)
-                *reinterpret_cast<float4*>(out + att_swz(j, 2 * m + h)) =
-                    make_float4(sc[m], sc[m + 4], sc[m + 8], sc[m + 12]);
+                for (int m = 0; m < 4; m++)
+                    *reinterpret_cast<float4*>(out + att_swz(j, 2 * m + h)) =
+                        make_float4(sc[m], sc[m + 4], sc[m + 8], sc[m + 12]);
+            } else {
+                float* out = G + (int64_t)kt * 1024;
+#pragma unroll
+                for (int m = 0; m < 4; m++)
+                    *reinterpret_cast<float4*>(out + att_swz(j, 2 * m + h)) =
+                        make_float4(sc[m], sc[m + 4], sc[m + 8], sc[m + 12]);
+            }
             if ((kt + 1) * 32 <= it.pos0 + 1) {
                 // below every row's first masked key; rows past q_count are never read back
 #pragma unroll
@@ -2900,11 +2926,24 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
                 }
             }
         };
-        for (int kt0 = k0; kt0 < k1; kt0 += NB) {
+        // this thread's float4 of tile kt: in the LDS below kt_cap, else in the spill region.
+        // A batch of NB tiles all in the LDS takes the LDS-only form of each loop below.
+        auto ldt = [&](int kt) -> float4 {
+            if (kt < kt_cap) return *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
+            return *reinterpret_cast<const float4*>(G + (int64_t)kt * 1024 + sw);
+        };
+        auto stt = [&](int kt, float4 v) {
+            if (kt < kt_cap) *reinterpret_cast<float4*>(S + kt * 1024 + sw) = v;
+            else *reinterpret_cast<float4*>(G + (int64_t)kt * 1024 + sw) = v;
+        };
+        auto e_batch = [&](int kt0, auto lds_only) {
             float4 sv[NB];
 #pragma unroll
-            for (int qq = 0; qq < NB; qq++)
-                sv[qq] = *reinterpret_cast<const float4*>(S + (kt0 + qq < k1 ? kt0 + qq : kt0) * 1024 + sw);
+            for (int qq = 0; qq < NB; qq++) {
+                const int kt = kt0 + qq < k1 ? kt0 + qq : kt0;
+                if constexpr (decltype(lds_only)::value) sv[qq] = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
+                else sv[qq] = ldt(kt);
+            }
 #pragma unroll
             for (int qq = 0; qq < NB; qq++) {
                 if (kt0 + qq >= k1) break;
@@ -2921,23 +2960,38 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
                         e[k] = qvalid && key < nq ? ex : 0.0f;
                     }
                 }
-                *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) = make_float4(e[0], e[1], e[2], e[3]);
+                const float4 ev = make_float4(e[0], e[1], e[2], e[3]);
+                if constexpr (decltype(lds_only)::value) *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) = ev;
+                else stt(kt0 + qq, ev);
                 if (p == 0) chain(kt0 + qq, e);
             }
+        };
+        for (int kt0 = k0; kt0 < k1; kt0 += NB) {
+            if constexpr (!SPILL) e_batch(kt0, std::true_type());
+            else if (kt0 + NB <= kt_cap) e_batch(kt0, std::true_type());
+            else e_batch(kt0, std::false_type());
         }
         __syncthreads();  // every e is written
         if (p == 0) {
-            for (int kt0 = kh; kt0 < n_kt; kt0 += NB) {
+            auto sum_batch = [&](int kt0, auto lds_only) {
                 float4 ev[NB];
 #pragma unroll
-                for (int qq = 0; qq < NB; qq++)
-                    ev[qq] = *reinterpret_cast<const float4*>(S + (kt0 + qq < n_kt ? kt0 + qq : kt0) * 1024 + sw);
+                for (int qq = 0; qq < NB; qq++) {
+                    const int kt = kt0 + qq < n_kt ? kt0 + qq : kt0;
+                    if constexpr (decltype(lds_only)::value) ev[qq] = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
+                    else ev[qq] = ldt(kt);
+                }
 #pragma unroll
                 for (int qq = 0; qq < NB; qq++) {
                     if (kt0 + qq >= n_kt) break;
                     const float e[4] = {ev[qq].x, ev[qq].y, ev[qq].z, ev[qq].w};
                     chain(kt0 + qq, e);
                 }
+            };
+            for (int kt0 = kh; kt0 < n_kt; kt0 += NB) {
+                if constexpr (!SPILL) sum_batch(kt0, std::true_type());
+                else if (kt0 + NB <= kt_cap) sum_batch(kt0, std::true_type());
+                else sum_batch(kt0, std::false_type());
             }
             float total = vsum8_lanes(lane_sum);
 #pragma unroll
@@ -2951,12 +3005,14 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
         if (qvalid) {
             const float total = tot[j];
             const float rcp = 1.0f / total;
-            for (int kt0 = k0; kt0 < k1; kt0 += 4) {
+            auto div_batch = [&](int kt0, auto lds_only) {
                 float e[16], w[16];
 #pragma unroll
                 for (int qq = 0; qq < 4; qq++) {
                     const int kt = kt0 + qq < k1 ? kt0 + qq : kt0;  // past the end: reread, not written
-                    const float4 v = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
+                    float4 v;
+                    if constexpr (decltype(lds_only)::value) v = *reinterpret_cast<const float4*>(S + kt * 1024 + sw);
+                    else v = ldt(kt);
                     e[4 * qq] = v.x;
                     e[4 * qq + 1] = v.y;
                     e[4 * qq + 2] = v.z;
@@ -2964,14 +3020,21 @@ __global__ __launch_bounds__(ATT_THREADS, 1) void k_attn_fused(const float* __re
                 }
                 softmax_divide<16>(e, w, total, rcp);
 #pragma unroll
-                for (int qq = 0; qq < 4; qq++)
-                    if (kt0 + qq < k1)
-                        *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) =
-                            make_float4(w[4 * qq], w[4 * qq + 1], w[4 * qq + 2], w[4 * qq + 3]);
+                for (int qq = 0; qq < 4; qq++) {
+                    if (kt0 + qq >= k1) continue;
+                    const float4 wv = make_float4(w[4 * qq], w[4 * qq + 1], w[4 * qq + 2], w[4 * qq + 3]);
+                    if constexpr (decltype(lds_only)::value) *reinterpret_cast<float4*>(S + (kt0 + qq) * 1024 + sw) = wv;
+                    else stt(kt0 + qq, wv);
+                }
+            };
+            for (int kt0 = k0; kt0 < k1; kt0 += 4) {
+                if constexpr (!SPILL) div_batch(kt0, std::true_type());
+                else if (kt0 + 4 <= kt_cap) div_batch(kt0, std::true_type());
+                else div_batch(kt0, std::false_type());
             }
         }
     }
-    attn_values_stream(vc, cap, it, kvh, head, n_kt, n_keys, S, ctx, ldc, ao);
+    attn_values_stream<SPILL>(vc, cap, it, kvh, head, n_kt, n_keys, S, G, kt_cap, ctx, ldc, ao);
 }
 
 // The softmax and value kernels of the three-kernel path take their work longest first
@@ -3086,20 +3149,26 @@ int attn_fused_kt_limit(int max_lds_bytes)
 
 hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
                              int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
-                             const ActQ8* codes, int kt_cap, hipStream_t s)
+                             const ActQ8* codes, int kt_cap, float* spill, hipStream_t s)
 {
     if (n_items <= 0) return hipSuccess;
     if (head_dim != ATT_HD || n_head % n_kv != 0 || n_head / n_kv > 4 || kt_cap <= 0) return hipErrorInvalidValue;
     if (codes && (codes->B != n_head * ATT_HD / 32 || !codes->q)) return hipErrorInvalidValue;
     const ActQ8 ao = codes ? *codes : ActQ8();
     const size_t lds = ((size_t)kt_cap * 1024 + ATT_RMAX + 32 + ATT_QLDS) * sizeof(float);
-    static LdsLimit limit;
-    hipError_t e = limit.raise(reinterpret_cast<const void*>(k_attn_fused), lds);
-    if (e != hipSuccess) return e;
+    static LdsLimit limit_lds, limit_spill;
     const int n_groups = n_items * n_kv;
     const unsigned grid = (unsigned)(((n_groups + 7) / 8) * 32);
-    hipLaunchKernelGGL(k_attn_fused, dim3(grid), dim3(ATT_THREADS), lds, s, q, ldq, kc, vc, cap, items, n_items, n_head, n_kv,
-                       scale, ctx, ldc, ao, kt_cap);
+    hipError_t e;
+    if (spill) {
+        if ((e = limit_spill.raise(reinterpret_cast<const void*>(k_attn_fused<true>), lds)) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_attn_fused<true>, dim3(grid), dim3(ATT_THREADS), lds, s, q, ldq, kc, vc, cap, items, n_items,
+                           n_head, n_kv, scale, ctx, ldc, ao, kt_cap, spill);
+    } else {
+        if ((e = limit_lds.raise(reinterpret_cast<const void*>(k_attn_fused<false>), lds)) != hipSuccess) return e;
+        hipLaunchKernelGGL(k_attn_fused<false>, dim3(grid), dim3(ATT_THREADS), lds, s, q, ldq, kc, vc, cap, items, n_items,
+                           n_head, n_kv, scale, ctx, ldc, ao, kt_cap, nullptr);
+    }
     return hipGetLastError();
 }
 

@@ -2,8 +2,9 @@
 131072): the 1024-token Q4_0 verdict and the 16-prompt ragged Q5_1 batch.
 
 Both are checked against the oracle at full size: the verdict's logits and its whole KV
-cache bit for bit, and, from the ragged batch, its longest prompt (1800 tokens: past 32
-key tiles, so the layers take the split softmax + values attention) and its shortest (90).
+cache bit for bit, and, from the ragged batch, its longest prompt (1800 tokens: past the 35
+key tiles a block's LDS holds, so the fused attention spills its later score tiles to the
+item's scratch region) and its shortest (90).
 The oracle runs on the host's threads on the weight bytes downloaded from the device;
 each of these takes well under a minute there. Size-independent properties back them:
 determinism, selected rows = full head, prefix cache = full pass, batch = single."""
