@@ -176,7 +176,7 @@ hipError_t launch_attn_pv(const float* vc, int cap, const AttnItem* items, int n
 // (the scratch regions place_items lays out) holds its later tiles; with spill null every
 // item must fit kt_cap tiles. Items of up to ATT_FUSED_MAX_KT key tiles take it; longer ones
 // the three kernels above.
-constexpr int ATT_FUSED_MAX_KT = 96;
+constexpr int ATT_FUSED_MAX_KT = 256;
 hipError_t launch_attn_fused(const float* q, int ldq, const float* kc, const float* vc, int cap, const AttnItem* items,
                              int n_items, int n_head, int n_kv, int head_dim, float scale, float* ctx, int ldc,
                              const ActQ8* codes, int kt_cap, float* spill, hipStream_t s);

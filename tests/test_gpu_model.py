@@ -54,15 +54,16 @@ def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
     """A 32-query item runs scores, softmax and values in one kernel (k_attn_fused), its
     first score tiles in the block's LDS (35 tiles of 32 keys beside the row maxima, the row
     sums and the 16 KB of query rows in 160 KB) and any later ones in the item's scratch
-    region; items past 96 key tiles take the three-kernel path. A pass of 1110 keys fills the
-    LDS exactly (35 tiles, the last partial), one of 1300 spills its last items' tiles past
-    the 35th, and one of 3100 runs both kernels in each layer (its last item, past 3072 keys,
-    through the three). All bit-exact, including a pass that starts mid-tile."""
+    region; items past 256 key tiles take the three-kernel path. A pass of 1110 keys fills the
+    LDS exactly (35 tiles, the last partial), ones of 1300 and 3100 spill their later items'
+    tiles past the 35th, and one of 8300 runs both kernels in each layer (its last items,
+    past 8192 keys, through the three). All bit-exact, including a pass that starts mid-tile."""
     cfg, tensors, types, gpu, ora = tiny
-    long_ora = oracle.OracleModel(cfg, tensors, types, cap=3200)
+    long_ora = oracle.OracleModel(cfg, tensors, types, cap=8400)
     rng = np.random.default_rng(11)
     ids = [1, 200, 511]
-    for prefix, n, fused in ((0, 70, True), (45, 50, True), (0, 1110, True), (0, 1300, True), (0, 3100, False)):
+    for prefix, n, fused in ((0, 70, True), (45, 50, True), (0, 1110, True), (0, 1300, True), (0, 3100, True),
+                             (0, 8300, False)):
         toks = rng.integers(0, cfg.vocab, prefix + n)
         gpu.reset_kv_cache()
         long_ora.reset()
@@ -84,24 +85,24 @@ def test_both_attention_paths_match_the_oracle(shs, oracle, tiny):
 
 def test_attention_with_two_query_heads_per_kv_head(shs, oracle):
     """GQA groups below 4: the score kernel leaves a block's extra waves idle and the fused
-    kernel skips the missing heads' blocks; both attention paths stay bit-exact (40-, 1100-
-    and 1300-token passes take the fused kernel, the last spilling tiles past the 35th; a
-    3100-token one also the three-kernel path)."""
+    kernel skips the missing heads' blocks; the attention stays bit-exact (40-, 1100-, 1300-
+    and 3100-token passes take the fused kernel, the last two spilling tiles past the 35th;
+    an 8300-token one also the three-kernel path)."""
     cfg = oracle.make_config(n_layer=1, hidden=256, n_head=4, n_kv_head=2, head_dim=128, ffn=512, vocab=512)
     tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=13)
     gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), tensors, types)
-    ora = oracle.OracleModel(cfg, tensors, types, cap=3200)
+    ora = oracle.OracleModel(cfg, tensors, types, cap=8400)
     rng = np.random.default_rng(17)
     ids = [0, 77, 300]
     try:
-        for n in (40, 1100, 1300, 3100):
+        for n in (40, 1100, 1300, 3100, 8300):
             toks = rng.integers(0, cfg.vocab, n)
             gpu.reset_kv_cache()
             ora.reset()
             g = gpu.forward_selected(toks, ids)
             o = ora.forward(toks, head_mode=1, vocab_ids=ids)
             assert np.array_equal(g, o), (n, H.rel_l2(g, o))
-        # decode width onto the 3100-token cache: 2 queries, then 1 (k_attn_dec_scores + k_attn_dec_pv)
+        # decode width onto the 8300-token cache: 2 queries, then 1 (k_attn_dec_scores + k_attn_dec_pv)
         gpu.profile(True)
         gpu.profile_reset()
         try:
@@ -121,8 +122,8 @@ def test_non_finite_score_rows_take_the_uniform_softmax(shs, oracle):
     finite (Kernels.cs:157-200). A huge attention-norm gain in layer 0 makes q·k overflow:
     at 1e19 some rows overflow and others stay finite, at 1e20 almost all overflow. The
     fused kernel (70 tokens; 1300, spilling score tiles past the LDS), the three-kernel path
-    (3100 tokens) and the decode-width kernels (one more token) must all match the oracle
-    bit for bit."""
+    (8300 tokens, its items past 256 key tiles) and the decode-width kernels (one more token)
+    must all match the oracle bit for bit."""
     cfg = oracle.make_config(**TINY)
     tensors, types = H.synth_model_tensors(oracle, cfg, 2, seed=7)
     rng = np.random.default_rng(23)
@@ -132,9 +133,9 @@ def test_non_finite_score_rows_take_the_uniform_softmax(shs, oracle):
         t2 = dict(tensors)
         t2["blk.0.attn_norm.weight"] = (tensors["blk.0.attn_norm.weight"] * np.float32(gain)).astype(np.float32)
         gpu = shs.MinistralModel.from_tensors(H.shs_config_from_oracle(shs, cfg), t2, types)
-        ora = oracle.OracleModel(cfg, t2, types, cap=3200)
+        ora = oracle.OracleModel(cfg, t2, types, cap=8400)
         try:
-            for n in (70, 1300, 3100):
+            for n in (70, 1300, 8300):
                 toks = rng.integers(0, cfg.vocab, n)
                 gpu.reset_kv_cache()
                 ora.reset()
@@ -143,10 +144,12 @@ def test_non_finite_score_rows_take_the_uniform_softmax(shs, oracle):
                 o = ora.forward(toks, head_mode=1, vocab_ids=ids, capture=lambda nm, a: cap.__setitem__(nm, a))
                 assert np.array_equal(g, o, equal_nan=True), (gain, n, H.rel_l2(g, o))
                 # the premise: layer 0's unscaled scores (exact in float64) pass FLT_MAX in some rows
-                q = cap["blk.0.q_rope"][:, :cfg.head_dim].astype(np.float64)
-                k = cap["blk.0.k_rope"][:, :cfg.head_dim].astype(np.float64)
+                # (checked over the first 1300 query rows)
+                m_rows = min(n, 1300)
+                q = cap["blk.0.q_rope"][:m_rows, :cfg.head_dim].astype(np.float64)
+                k = cap["blk.0.k_rope"][:m_rows, :cfg.head_dim].astype(np.float64)
                 s = np.abs(q @ k.T)
-                row_max = np.array([s[i, :i + 1].max() for i in range(n)])
+                row_max = np.array([s[i, :i + 1].max() for i in range(m_rows)])
                 over = row_max > flt_max
                 assert over.any(), (gain, n)
                 if mixed:
