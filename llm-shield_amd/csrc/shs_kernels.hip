@@ -1311,8 +1311,9 @@ __global__ __launch_bounds__(256, (gemm_wg_per_cu<TYPE, TT, BPS>())) void k_gemm
         // Rope.Apply on adjacent pairs (x0, x1) → (x0c − x1s, x0s + x1c), unfused, then the
         // query position scale (MinistralModel.cs:442-482); StoreKeys/StoreValues put k and v
         // at the token's cache slot. A tile lies inside one head (hd is a multiple of 32).
-        // The tile goes through this wave's part of the ring as [token][32 features], so that
-        // every store below writes whole 128-byte rows (8 tokens per instruction).
+        // The tile goes through this wave's part of the ring as [token][32 features]; read back
+        // as 8 lanes per token (4 features each), the rotation's table reads and the stores
+        // below each touch 8 token rows per instruction, the stores in whole 128-byte rows.
         constexpr int XLD = 36;  // floats per staged token row: rows start 4 banks apart
         static_assert(NS * L::BYTES >= 4 * TT * 32 * XLD * 4, "the ring holds the staged tiles");
         float* X = reinterpret_cast<float*>(ring) + wave * TT * 32 * XLD;
@@ -1320,40 +1321,15 @@ __global__ __launch_bounds__(256, (gemm_wg_per_cu<TYPE, TT, BPS>())) void k_gemm
         const bool rot = hrow < ra.n_head + ra.n_kv, query = hrow < ra.n_head;
 #pragma unroll
         for (int u = 0; u < TT; u++) {
-            const int token = (tt0 + u) * 32 + j;
-            if (u >= nv || token >= a.T) continue;
-            const int p = ra.pos[token];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const int e = e0 + 8 * g + 4 * h;  // element of the head held in acc[u][4g..4g+3]
-                float v[4] = {acc[u][4 * g], acc[u][4 * g + 1], acc[u][4 * g + 2], acc[u][4 * g + 3]};
-                if (rot) {
-#pragma unroll
-                    for (int k = 0; k < 2; k++) {
-                        const int pi = e / 2 + k;
-                        if (pi < ra.half) {
-                            const float c = ra.ct[(int64_t)p * ra.half + pi], sn = ra.st[(int64_t)p * ra.half + pi];
-                            const float x0 = v[2 * k], x1 = v[2 * k + 1];
-                            const float a0 = x0 * c, b0 = x1 * sn;
-                            const float e1 = x0 * sn, f1 = x1 * c;
-                            v[2 * k] = a0 - b0;
-                            v[2 * k + 1] = e1 + f1;
-                        }
-                    }
-                }
-                if (query) {
-                    const float qs = ra.qscale[p];
-                    if (qs != 1.0f) {
-#pragma unroll
-                        for (int k = 0; k < 4; k++) v[k] = v[k] * qs;
-                    }
-                }
-                *reinterpret_cast<float4*>(X + (u * 32 + j) * XLD + 8 * g + 4 * h) = make_float4(v[0], v[1], v[2], v[3]);
-            }
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4*>(X + (u * 32 + j) * XLD + 8 * g + 4 * h) =
+                    make_float4(acc[u][4 * g], acc[u][4 * g + 1], acc[u][4 * g + 2], acc[u][4 * g + 3]);
         }
         // this wave's rows are in the LDS (only this wave reads them)
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const int c4 = 4 * (lane & 7);
+        const int pi0 = (e0 + c4) / 2;  // this lane's two pairs of the head: pi0, pi0 + 1
 #pragma unroll
         for (int u = 0; u < TT; u++) {
 #pragma unroll
@@ -1361,7 +1337,33 @@ __global__ __launch_bounds__(256, (gemm_wg_per_cu<TYPE, TT, BPS>())) void k_gemm
                 const int r = (lane >> 3) + 8 * i;
                 const int token = (tt0 + u) * 32 + r;
                 if (u >= nv || token >= a.T) continue;
-                const float4 v = *reinterpret_cast<const float4*>(X + (u * 32 + r) * XLD + c4);
+                const float4 x = *reinterpret_cast<const float4*>(X + (u * 32 + r) * XLD + c4);
+                float v[4] = {x.x, x.y, x.z, x.w};
+                if (rot || query) {
+                    const int p = ra.pos[token];
+                    if (rot) {
+#pragma unroll
+                        for (int k = 0; k < 2; k++) {
+                            const int pi = pi0 + k;
+                            if (pi < ra.half) {
+                                const float c = ra.ct[(int64_t)p * ra.half + pi], sn = ra.st[(int64_t)p * ra.half + pi];
+                                const float x0 = v[2 * k], x1 = v[2 * k + 1];
+                                const float a0 = x0 * c, b0 = x1 * sn;
+                                const float e1 = x0 * sn, f1 = x1 * c;
+                                v[2 * k] = a0 - b0;
+                                v[2 * k + 1] = e1 + f1;
+                            }
+                        }
+                    }
+                    if (query) {
+                        const float qs = ra.qscale[p];
+                        if (qs != 1.0f) {
+#pragma unroll
+                            for (int k = 0; k < 4; k++) v[k] = v[k] * qs;
+                        }
+                    }
+                }
+                const float4 vo = make_float4(v[0], v[1], v[2], v[3]);
                 float* dst;
                 if (query)
                     dst = y + (int64_t)token * ldy + rt * 32 + c4;
@@ -1369,7 +1371,7 @@ __global__ __launch_bounds__(256, (gemm_wg_per_cu<TYPE, TT, BPS>())) void k_gemm
                     dst = ra.kc + ((int64_t)(hrow - ra.n_head) * ra.cap + ra.slot0 + token) * ra.hd + e0 + c4;
                 else
                     dst = ra.vc + ((int64_t)(hrow - ra.n_head - ra.n_kv) * ra.cap + ra.slot0 + token) * ra.hd + e0 + c4;
-                *reinterpret_cast<float4*>(dst) = v;
+                *reinterpret_cast<float4*>(dst) = vo;
             }
         }
         return;
